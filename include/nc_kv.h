@@ -1,0 +1,163 @@
+/*
+ * nc_kv.h -- C ABI of libnc_kv.so, the MI355X (gfx950) KV-cache inference path.
+ *
+ * The library replaces the compute inside nanochat's inference KV-cache path:
+ *   - nanochat/flash_attention.py:131-177  flash_attn_with_kvcache (append + attention)
+ *   - nanochat/flash_attention.py:69-102   _sdpa_attention masks (causal, sliding window, GQA)
+ *   - nanochat/engine.py:123-137           KVCache.prefill (broadcast fan-out copy)
+ * Host code (Python, ctypes) validates shapes and dtypes, then calls these
+ * functions with raw device pointers, element strides and the caller's stream.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer (hipMalloc'd / torch CUDA tensor data).
+ *   - Strides are in ELEMENTS of the tensor they describe; the innermost
+ *     (head_dim) stride is always 1.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the null stream.
+ *   - Nothing here synchronises the host or allocates memory.
+ *   - Return value: NC_OK (0) or an nc_status code; nc_strerror() names it.
+ */
+#ifndef NC_KV_H
+#define NC_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NC_KV_ABI_VERSION 1
+
+/* Element types (the torch dtypes the reference path uses). */
+enum nc_dtype {
+  NC_DTYPE_F32 = 0,
+  NC_DTYPE_F16 = 1,
+  NC_DTYPE_BF16 = 2
+};
+
+enum nc_status {
+  NC_OK = 0,
+  NC_ERR_NULL_ARG = 1,          /* a required pointer is NULL               */
+  NC_ERR_BAD_SHAPE = 2,         /* a size is <= 0 or inconsistent           */
+  NC_ERR_DTYPE = 3,             /* unsupported dtype combination            */
+  NC_ERR_HEAD_DIM = 4,          /* head_dim not in the compiled set         */
+  NC_ERR_ALIGNMENT = 5,         /* pointer / stride not 16-byte aligned     */
+  NC_ERR_WORKSPACE = 6,         /* workspace NULL or smaller than required  */
+  NC_ERR_LAUNCH = 7             /* hipLaunchKernel / hipGetLastError failed */
+};
+
+/* Bit set in *error_flag by a kernel when a row would write past t_max
+ * (cache_seqlens[b] + t_new > t_max).  Such writes are skipped, never done
+ * out of bounds.  The reference raises a torch size-mismatch RuntimeError at
+ * nanochat/flash_attention.py:161 for the same condition. */
+#define NC_DEVERR_OVERFLOW 1
+
+/* ---------------------------------------------------------------------------
+ * Ragged KV append: k_cache[b, cache_seqlens[b] + t] = k[b, t] (and v), t < t_new.
+ * Replaces nanochat/flash_attention.py:160-162 with FA3's per-row positions
+ * (the fallback uses row 0's position for every row).  Values are converted
+ * to the cache dtype with round-to-nearest-even (NaN -> canonical quiet NaN),
+ * exactly as torch's copy_ does.  cache_seqlens is read, never written.
+ * ------------------------------------------------------------------------- */
+typedef struct nc_append_args {
+  void* k_cache;                 /* (B, T_max, H_kv, D) */
+  void* v_cache;
+  const void* k;                 /* (B, T_new, H_kv, D) */
+  const void* v;
+  const int32_t* cache_seqlens;  /* (B,) */
+  int32_t* error_flag;           /* optional (NULL): NC_DEVERR_* bits are OR-ed in */
+  int64_t batch, t_new, t_max, n_kv_heads, head_dim;
+  int64_t kc_stride_b, kc_stride_t, kc_stride_h;
+  int64_t vc_stride_b, vc_stride_t, vc_stride_h;
+  int64_t k_stride_b, k_stride_t, k_stride_h;
+  int64_t v_stride_b, v_stride_t, v_stride_h;
+  int32_t in_dtype;              /* dtype of k, v */
+  int32_t cache_dtype;           /* dtype of k_cache, v_cache */
+} nc_append_args;
+
+int nc_kv_append(const nc_append_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Prefill fan-out: for every layer l and destination row n < n_rows,
+ *   dst[l, n, 0:prefix_len] = src[l, 0, 0:prefix_len]     (K and V)
+ * and, if dst_seqlens != NULL, dst_seqlens[n] = prefix_len.
+ * Replaces nanochat/engine.py:132-134.  One launch covers K and V of every
+ * layer; each source byte is read once and written n_rows times.
+ * Each [l, row, 0:prefix_len] region must be contiguous (row_elems = H_kv*D
+ * elements per token), which holds for KVCache's (L, B, T, H_kv, D) slabs.
+ * ------------------------------------------------------------------------- */
+typedef struct nc_fanout_args {
+  const void* k_src;             /* (L, 1, T_src, H_kv, D) */
+  const void* v_src;
+  void* k_dst;                   /* (L, N, T_dst, H_kv, D) */
+  void* v_dst;
+  int32_t* dst_seqlens;          /* optional (N,) */
+  int64_t n_layers, n_rows, prefix_len, row_elems;
+  int64_t src_stride_l;          /* elements between layers of src        */
+  int64_t dst_stride_l;          /* elements between layers of dst        */
+  int64_t dst_stride_b;          /* elements between rows of dst          */
+  int32_t dtype;                 /* same dtype for src and dst            */
+} nc_fanout_args;
+
+int nc_kv_fanout(const nc_fanout_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * flash_attn_with_kvcache: optional append of (k, v) at cache_seqlens, then
+ *   out[b,i,h] = softmax_j( q[b,i,h] . K[b,j,h/G] * scale ) . V[b,j,h/G]
+ * over keys j with  j <= s_b + i  and  (window_left < 0 || s_b + i - j <= window_left),
+ * where s_b = cache_seqlens[b] and G = n_heads / n_kv_heads.
+ * This is nanochat/flash_attention.py:155-177 + :69-102 (queries bottom-right
+ * aligned, row_idx = Tk - Tq + i) applied with each row's own s_b.
+ * `causal` is accepted and, like the reference fallback, does not change the
+ * mask.  Output is (B, T_new, H, D), contiguous, in q's dtype; accumulation
+ * is fp32.  The fused path (t_new == 1) appends and attends in one launch;
+ * t_new > 1 appends first and then attends (two launches, same stream).
+ * The workspace holds split-K partials and per-(row, head) counters: it must
+ * be zero-filled before its first use and is left zeroed by every call, so a
+ * caller keeps one workspace per stream.  Calls sharing a workspace must not
+ * overlap in time (different streams need different workspaces).
+ * ------------------------------------------------------------------------- */
+typedef struct nc_attn_args {
+  const void* q;                 /* (B, T_new, H, D) */
+  void* out;                     /* (B, T_new, H, D) contiguous */
+  void* k_cache;                 /* (B, T_max, H_kv, D) */
+  void* v_cache;
+  const void* k;                 /* (B, T_new, H_kv, D) or NULL (no append) */
+  const void* v;
+  const int32_t* cache_seqlens;  /* (B,) read-only */
+  int32_t* error_flag;           /* optional */
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t batch, t_new, t_max, n_heads, n_kv_heads, head_dim;
+  int64_t q_stride_b, q_stride_t, q_stride_h;
+  int64_t kc_stride_b, kc_stride_t, kc_stride_h;
+  int64_t vc_stride_b, vc_stride_t, vc_stride_h;
+  int64_t k_stride_b, k_stride_t, k_stride_h;
+  int64_t v_stride_b, v_stride_t, v_stride_h;
+  int32_t window_left;           /* < 0: unlimited */
+  int32_t causal;
+  float softmax_scale;           /* nanochat: head_dim ** -0.5 */
+  int32_t q_dtype;               /* dtype of q, k, v and out */
+  int32_t cache_dtype;
+  int32_t keys_per_split;        /* 0: library default; else a multiple of 64 */
+} nc_attn_args;
+
+/* Bytes of workspace nc_attn_kvcache needs for these arguments. */
+size_t nc_attn_workspace_bytes(const nc_attn_args* args);
+
+int nc_attn_kvcache(const nc_attn_args* args, void* stream);
+
+/* Name of an nc_status code (static string). */
+const char* nc_strerror(int status);
+
+/* NC_KV_ABI_VERSION of the built library. */
+int nc_abi_version(void);
+
+/* Non-zero if the library was built with kernels for `head_dim`. */
+int nc_supports_head_dim(int64_t head_dim);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NC_KV_H */

@@ -1,0 +1,155 @@
+"""ctypes binding of libnc_kv.so (declared in include/nc_kv.h).
+
+Loads the in-tree library built by ``python -m nanochat_amd.build`` and
+mirrors its argument structs.  There is no fallback: if the library is
+missing, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libnc_kv.so"
+ABI_VERSION = 1
+
+DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+NC_DEVERR_OVERFLOW = 1
+
+_c_void_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+
+class AppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("k_cache", _c_void_p), ("v_cache", _c_void_p),
+        ("k", _c_void_p), ("v", _c_void_p),
+        ("cache_seqlens", _c_void_p), ("error_flag", _c_void_p),
+        ("batch", _i64), ("t_new", _i64), ("t_max", _i64), ("n_kv_heads", _i64), ("head_dim", _i64),
+        ("kc_stride_b", _i64), ("kc_stride_t", _i64), ("kc_stride_h", _i64),
+        ("vc_stride_b", _i64), ("vc_stride_t", _i64), ("vc_stride_h", _i64),
+        ("k_stride_b", _i64), ("k_stride_t", _i64), ("k_stride_h", _i64),
+        ("v_stride_b", _i64), ("v_stride_t", _i64), ("v_stride_h", _i64),
+        ("in_dtype", _i32), ("cache_dtype", _i32),
+    ]
+
+
+class FanoutArgs(ctypes.Structure):
+    _fields_ = [
+        ("k_src", _c_void_p), ("v_src", _c_void_p),
+        ("k_dst", _c_void_p), ("v_dst", _c_void_p),
+        ("dst_seqlens", _c_void_p),
+        ("n_layers", _i64), ("n_rows", _i64), ("prefix_len", _i64), ("row_elems", _i64),
+        ("src_stride_l", _i64), ("dst_stride_l", _i64), ("dst_stride_b", _i64),
+        ("dtype", _i32),
+    ]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _c_void_p), ("out", _c_void_p),
+        ("k_cache", _c_void_p), ("v_cache", _c_void_p),
+        ("k", _c_void_p), ("v", _c_void_p),
+        ("cache_seqlens", _c_void_p), ("error_flag", _c_void_p),
+        ("workspace", _c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("batch", _i64), ("t_new", _i64), ("t_max", _i64),
+        ("n_heads", _i64), ("n_kv_heads", _i64), ("head_dim", _i64),
+        ("q_stride_b", _i64), ("q_stride_t", _i64), ("q_stride_h", _i64),
+        ("kc_stride_b", _i64), ("kc_stride_t", _i64), ("kc_stride_h", _i64),
+        ("vc_stride_b", _i64), ("vc_stride_t", _i64), ("vc_stride_h", _i64),
+        ("k_stride_b", _i64), ("k_stride_t", _i64), ("k_stride_h", _i64),
+        ("v_stride_b", _i64), ("v_stride_t", _i64), ("v_stride_h", _i64),
+        ("window_left", _i32), ("causal", _i32),
+        ("softmax_scale", ctypes.c_float),
+        ("q_dtype", _i32), ("cache_dtype", _i32),
+        ("keys_per_split", _i32),
+    ]
+
+
+# Every function include/nc_kv.h declares, with its ctypes signature.
+EXPORTS = {
+    "nc_abi_version": (ctypes.c_int, []),
+    "nc_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "nc_supports_head_dim": (ctypes.c_int, [_i64]),
+    "nc_kv_append": (ctypes.c_int, [ctypes.POINTER(AppendArgs), _c_void_p]),
+    "nc_kv_fanout": (ctypes.c_int, [ctypes.POINTER(FanoutArgs), _c_void_p]),
+    "nc_attn_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
+    "nc_attn_kvcache": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _c_void_p]),
+}
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded libnc_kv.so (raises RuntimeError if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with `python -m nanochat_amd.build` "
+                    "(the KV-cache path has no non-HIP implementation)")
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, argtypes) in EXPORTS.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = argtypes
+            if handle.nc_abi_version() != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH} has ABI {handle.nc_abi_version()}, expected {ABI_VERSION}")
+            _lib = handle
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = lib().nc_strerror(status).decode()
+        raise RuntimeError(f"{what} failed: {msg} (nc_status {status})")
+
+
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on `device`, as an integer."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# ---------------------------------------------------------------------------
+# Per-(device, stream) split-K workspace and per-device error flag.
+# The kernels leave the workspace's ticket counters at zero, so one zeroed
+# buffer per stream is reused across calls; calls on one stream are ordered.
+# ---------------------------------------------------------------------------
+_workspaces: dict = {}
+_error_flags: dict = {}
+
+
+def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
+    if nbytes == 0:
+        return None
+    key = (device.index, stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        cap = max(nbytes, 2 * buf.numel() if buf is not None else 0, 1 << 20)
+        buf = torch.zeros(cap, dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf
+
+
+def error_flag(device: torch.device) -> torch.Tensor:
+    flag = _error_flags.get(device.index)
+    if flag is None:
+        flag = torch.zeros(1, dtype=torch.int32, device=device)
+        _error_flags[device.index] = flag
+    return flag
+
+
+def read_and_clear_device_errors(device: torch.device) -> int:
+    """NC_DEVERR_* bits raised by kernels on `device` since the last read (synchronises)."""
+    flag = error_flag(device)
+    bits = int(flag.item())
+    flag.zero_()
+    return bits

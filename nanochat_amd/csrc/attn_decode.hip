@@ -1,0 +1,448 @@
+// Split-K flash-decoding over the KV cache (nanochat/flash_attention.py:82-89,
+// 155-177 with FA3's per-row cache_seqlens), GQA and sliding window.
+//
+// Work decomposition: one workgroup per (row b, query t, kv head, q-head block,
+// key split).  A split is a contiguous run of `keys_per_split` cache positions
+// of one kv head; the workgroup streams it once from HBM and scores it against
+// every q head of its head block (GQA packing: the K/V bytes are read once for
+// all G = H / H_kv query heads).
+//
+// Lane layout inside a wave (D = head_dim, VEC = elements per 16 bytes):
+//   LPK = D / VEC lanes hold one key row (16 bytes each), KPI = 64 / LPK keys
+//   are covered by one 128-bit load instruction.  q . k is a per-lane partial
+//   dot product finished by a DPP all-reduce over the LPK lanes, so every lane
+//   of a key group ends up with that key's score and no LDS traffic is needed
+//   in the streaming loop.  Each key group (`row`) keeps its own online-softmax
+//   state (max m, sum l, output o) and rows / waves are merged once at the end.
+//
+// Split merge: a split writes (o, m, l) partials to the workspace; the last
+// workgroup of a (b, t, kv head, head block) to finish (atomic ticket) merges
+// them with the log-sum-exp rule and writes the output, then re-zeroes its
+// ticket.  Single-split rows write the output directly.
+//
+// Fused append (t_new == 1 with k/v given): the split owning position s_b
+// takes the new key/value from the k/v inputs (converted to the cache dtype,
+// RNE) instead of the cache, and head block 0 stores them into the cache.  No
+// other workgroup reads position s_b, so the store does not race.
+
+#include "nc_kv_common.hpp"
+#include "nc_kv_internal.hpp"
+
+namespace nckv {
+
+namespace {
+
+constexpr int kWavesPerWG = 4;
+constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for running maxima
+
+struct DecodeParams {
+  const void* q;
+  void* out;
+  char* kc;
+  char* vc;
+  const void* k_new;
+  const void* v_new;
+  const int32_t* seqlens;
+  int32_t* err;
+  int32_t* counters;
+  float* part_ml;
+  float* part_o;
+  int64_t q_sb, q_st, q_sh;
+  int64_t kc_sb, kc_st, kc_sh;
+  int64_t vc_sb, vc_st, vc_sh;
+  int64_t k_sb, k_st, k_sh;
+  int64_t v_sb, v_st, v_sh;
+  int32_t t_new, t_max, n_heads, n_kv_heads, group, n_hblocks;
+  int32_t window;
+  float scale_log2;
+  int32_t q_dtype;
+  int32_t num_splits, keys_per_split;
+  int32_t fused;
+};
+
+template <typename TC> struct dot_packed;
+template <> struct dot_packed<bf16> {
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float run(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+};
+template <> struct dot_packed<f16> {
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  __device__ __forceinline__ static float run(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+};
+
+// Query fragment of one lane for one head: either the raw 16-byte vector in
+// the cache dtype (QPK, packed dot2 path) or VEC fp32 values.
+template <typename TC, bool QPK> struct QFrag;
+template <typename TC> struct QFrag<TC, true> {
+  uint4 w;
+  __device__ __forceinline__ float dot(const uint4& k) const {
+    float acc = dot_packed<TC>::run(w.x, k.x, 0.0f);
+    acc = dot_packed<TC>::run(w.y, k.y, acc);
+    acc = dot_packed<TC>::run(w.z, k.z, acc);
+    acc = dot_packed<TC>::run(w.w, k.w, acc);
+    return acc;
+  }
+};
+template <typename TC> struct QFrag<TC, false> {
+  static constexpr int VEC = widen<TC>::N;
+  float f[VEC];
+  __device__ __forceinline__ float dot(const uint4& k) const {
+    float kf[VEC];
+    widen<TC>::run(k, kf);
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc = __builtin_fmaf(f[e], kf[e], acc);
+    return acc;
+  }
+};
+
+template <typename TC, bool QPK, int D, int GB>
+__global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const DecodeParams p) {
+  constexpr int VEC = widen<TC>::N;
+  constexpr int LPK = D / VEC;            // lanes per key row
+  constexpr int KPI = kWave / LPK;        // keys per load instruction
+  constexpr int NI = (GB >= 4) ? 4 : 8;   // load instructions per tile (K and V each)
+  constexpr int TILE = KPI * NI;          // keys per wave tile
+  constexpr int NW = kWavesPerWG;
+  constexpr int EB = elem<TC>::kBytes;
+  static_assert(LPK >= 1 && LPK <= kWave && KPI * LPK == kWave, "head_dim / dtype");
+
+  __shared__ float sm_o[NW][GB][D];
+  __shared__ float sm_m[NW][GB];
+  __shared__ float sm_l[NW][GB];
+  __shared__ float sm_w[NW][GB];
+  __shared__ float sm_L[GB];
+  __shared__ int sm_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int row = lane / LPK;
+  const int col = lane % LPK;
+
+  // ---- block -> (b, t, kv head, head block, split) ----
+  int64_t wg = blockIdx.x;
+  const int split = static_cast<int>(wg % p.num_splits); wg /= p.num_splits;
+  const int hb = static_cast<int>(wg % p.n_hblocks); wg /= p.n_hblocks;
+  const int hk = static_cast<int>(wg % p.n_kv_heads); wg /= p.n_kv_heads;
+  const int t = static_cast<int>(wg % p.t_new);
+  const int64_t b = wg / p.t_new;
+
+  const int s = p.seqlens[b];
+  const int qpos = s + t;                         // absolute position of the query
+  const int hi = min(qpos + 1, p.t_max);          // keys [lo, hi)
+  const int lo = p.window >= 0 ? max(0, qpos - p.window) : 0;
+  const int n = hi - lo;
+  const int nsplit = n > 0 ? (n + p.keys_per_split - 1) / p.keys_per_split : 1;
+  if (split >= nsplit) return;
+
+  const int k0 = lo + split * p.keys_per_split;
+  const int k1 = n > 0 ? min(k0 + p.keys_per_split, hi) : k0;
+  const bool new_in_range = p.fused && qpos >= 0 && qpos < p.t_max;
+  const bool own_new = new_in_range && n > 0 && k1 == qpos + 1;
+  const int kc_end = own_new ? k1 - 1 : k1;       // keys read from the cache: [k0, kc_end)
+
+  if (p.fused && (qpos < 0 || qpos >= p.t_max) && split == 0 && hb == 0 && tid == 0 && p.err != nullptr) {
+    atomicOr(p.err, NC_DEVERR_OVERFLOW);
+  }
+
+  const int h0 = hk * p.group + hb * GB;          // first q head of this block
+
+  // ---- query fragments ----
+  QFrag<TC, QPK> qf[GB];
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    const int64_t qoff = b * p.q_sb + t * p.q_st + (h0 + g) * p.q_sh + col * VEC;
+    if constexpr (QPK) {
+      qf[g].w = *reinterpret_cast<const uint4*>(static_cast<const char*>(p.q) + qoff * EB);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qf[g].f[e] = load_any(p.q, qoff + e, p.q_dtype);
+    }
+  }
+
+  float m[GB], l[GB], o[GB][VEC];
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) o[g][e] = 0.0f;
+  }
+
+  const char* kbase = p.kc + (b * p.kc_sb + hk * p.kc_sh + col * VEC) * EB;
+  const char* vbase = p.vc + (b * p.vc_sb + hk * p.vc_sh + col * VEC) * EB;
+  const int64_t kst = p.kc_st * EB;
+  const int64_t vst = p.vc_st * EB;
+
+  // ---- stream the split's cache keys, TILE keys per wave per step ----
+  for (int base = k0 + wave * TILE; base < kc_end; base += NW * TILE) {
+    uint4 kv[NI], vv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int j = base + i * KPI + row;
+      if (j < kc_end) {
+        kv[i] = *reinterpret_cast<const uint4*>(kbase + j * kst);
+        vv[i] = *reinterpret_cast<const uint4*>(vbase + j * vst);
+      } else {
+        kv[i] = make_uint4(0, 0, 0, 0);
+        vv[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    float sc[GB][NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const bool valid = base + i * KPI + row < kc_end;
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        const float d = group_sum<LPK>(qf[g].dot(kv[i])) * p.scale_log2;
+        sc[g][i] = valid ? d : -__builtin_inff();
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      float mt = sc[g][0];
+#pragma unroll
+      for (int i = 1; i < NI; ++i) mt = fmaxf(mt, sc[g][i]);
+      const float mn = fmaxf(m[g], mt);
+      const float alpha = fast_exp2(m[g] - mn);
+      m[g] = mn;
+      l[g] *= alpha;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[g][e] *= alpha;
+    }
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      float vf[VEC];
+      widen<TC>::run(vv[i], vf);
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        const float pr = fast_exp2(sc[g][i] - m[g]);
+        l[g] += pr;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[g][e] = __builtin_fmaf(pr, vf[e], o[g][e]);
+      }
+    }
+  }
+
+  // ---- the appended token (fused path): read from k/v, store into the cache ----
+  if (own_new && wave == NW - 1) {
+    const int64_t koff = b * p.k_sb + hk * p.k_sh + col * VEC;
+    const int64_t voff = b * p.v_sb + hk * p.v_sh + col * VEC;
+    const uint4 kn = load_as_cache_vec<TC>(p.k_new, koff, p.q_dtype);
+    const uint4 vn = load_as_cache_vec<TC>(p.v_new, voff, p.q_dtype);
+    if (hb == 0 && row == 0) {
+      *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + qpos * kst) = kn;
+      *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + qpos * vst) = vn;
+    }
+    float vf[VEC];
+    widen<TC>::run(vn, vf);
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      const float d = group_sum<LPK>(qf[g].dot(kn)) * p.scale_log2;
+      const float sc = row == 0 ? d : -__builtin_inff();
+      const float mn = fmaxf(m[g], sc);
+      const float alpha = fast_exp2(m[g] - mn);
+      const float pr = fast_exp2(sc - mn);
+      m[g] = mn;
+      l[g] = l[g] * alpha + pr;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) o[g][e] = __builtin_fmaf(pr, vf[e], o[g][e] * alpha);
+    }
+  }
+
+  // ---- merge the KPI key groups of each wave (butterfly over lane offsets LPK..32) ----
+#pragma unroll
+  for (int off = LPK; off < kWave; off *= 2) {
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+      const float mo = __shfl_xor(m[g], off, kWave);
+      const float lo_ = __shfl_xor(l[g], off, kWave);
+      const float mn = fmaxf(m[g], mo);
+      const float a_self = fast_exp2(m[g] - mn);
+      const float a_other = fast_exp2(mo - mn);
+      l[g] = l[g] * a_self + lo_ * a_other;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const float oo = __shfl_xor(o[g][e], off, kWave);
+        o[g][e] = o[g][e] * a_self + oo * a_other;
+      }
+      m[g] = mn;
+    }
+  }
+  if (row == 0) {
+#pragma unroll
+    for (int g = 0; g < GB; ++g) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) sm_o[wave][g][col * VEC + e] = o[g][e];
+      if (col == 0) {
+        sm_m[wave][g] = m[g];
+        sm_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- merge the waves ----
+  if (tid < GB) {
+    const int g = tid;
+    float mx = sm_m[0][g];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, sm_m[w][g]);
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = fast_exp2(sm_m[w][g] - mx);
+      sm_w[w][g] = wt;
+      L += sm_l[w][g] * wt;
+    }
+    sm_L[g] = L;
+    sm_m[0][g] = mx;  // keep the merged max in slot 0 (read below)
+  }
+  __syncthreads();
+
+  const int64_t pair0 = (b * p.t_new + t) * p.n_heads + h0;  // (b, t, h0)
+  if (nsplit == 1) {
+    for (int idx = tid; idx < GB * D; idx += NW * kWave) {
+      const int g = idx / D, d = idx % D;
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) acc += sm_o[w][g][d] * sm_w[w][g];
+      const float L = sm_L[g];
+      store_any(p.out, (pair0 + g) * D + d, p.q_dtype, L > 0.0f ? acc / L : 0.0f);
+    }
+    return;
+  }
+
+  for (int idx = tid; idx < GB * D; idx += NW * kWave) {
+    const int g = idx / D, d = idx % D;
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) acc += sm_o[w][g][d] * sm_w[w][g];
+    p.part_o[((pair0 + g) * p.num_splits + split) * D + d] = acc;
+  }
+  if (tid < GB) {
+    float* ml = p.part_ml + ((pair0 + tid) * p.num_splits + split) * 2;
+    ml[0] = sm_m[0][tid];
+    ml[1] = sm_L[tid];
+  }
+
+  // ---- last split of this (b, t, kv head, head block) merges all partials ----
+  __threadfence();
+  __syncthreads();
+  const int64_t ctr = ((b * p.t_new + t) * p.n_kv_heads + hk) * p.n_hblocks + hb;
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(p.counters + ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    sm_last = (prev == nsplit - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!sm_last) return;
+  __threadfence();
+
+  // sm_o[0] is reused to hold per-split weights: (g, split) for split < nsplit.
+  float* wts = &sm_o[0][0][0];
+  const int wcap = NW * GB * D / GB;  // weights slots per head
+  if (tid < GB) {
+    const int g = tid;
+    const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
+    float mx = kNegBig;
+    for (int sp = 0; sp < nsplit; ++sp) {
+      mx = fmaxf(mx, __hip_atomic_load(ml + 2 * sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    }
+    float L = 0.0f;
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float ms = __hip_atomic_load(ml + 2 * sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float ls = __hip_atomic_load(ml + 2 * sp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float wt = fast_exp2(ms - mx);
+      if (sp < wcap) wts[g * wcap + sp] = wt;
+      L += ls * wt;
+    }
+    sm_L[g] = L;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < GB * D; idx += NW * kWave) {
+    const int g = idx / D, d = idx % D;
+    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d;
+    float acc = 0.0f;
+    for (int sp = 0; sp < nsplit; ++sp) acc += po[static_cast<int64_t>(sp) * D] * wts[g * wcap + sp];
+    const float L = sm_L[g];
+    store_any(p.out, (pair0 + g) * D + d, p.q_dtype, L > 0.0f ? acc / L : 0.0f);
+  }
+  if (tid == 0) __hip_atomic_store(p.counters + ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename TC, bool QPK, int D>
+hipError_t launch_d(const DecodeParams& p, int gb, int64_t n_wg, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(n_wg));
+  const dim3 block(kWavesPerWG * kWave);
+  switch (gb) {
+    case 8: hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, 8>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, 4>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, 2>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, 1>), grid, block, 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
+template <typename TC, bool QPK>
+hipError_t launch_dt(const DecodeParams& p, int64_t head_dim, int gb, int64_t n_wg, hipStream_t stream) {
+  switch (head_dim) {
+    case 32: return launch_d<TC, QPK, 32>(p, gb, n_wg, stream);
+    case 64: return launch_d<TC, QPK, 64>(p, gb, n_wg, stream);
+    case 128: return launch_d<TC, QPK, 128>(p, gb, n_wg, stream);
+    default: return launch_d<TC, QPK, 256>(p, gb, n_wg, stream);
+  }
+}
+
+}  // namespace
+
+bool decode_supports(int cache_dtype, int64_t head_dim) {
+  (void)cache_dtype;
+  return head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
+}
+
+int split_weight_capacity(int64_t head_dim) { return kWavesPerWG * static_cast<int>(head_dim); }
+
+hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
+                         bool fused_append, hipStream_t stream) {
+  DecodeParams p;
+  p.q = a.q; p.out = a.out;
+  p.kc = static_cast<char*>(a.k_cache); p.vc = static_cast<char*>(a.v_cache);
+  p.k_new = a.k; p.v_new = a.v;
+  p.seqlens = a.cache_seqlens; p.err = a.error_flag;
+  p.counters = s.counters; p.part_ml = s.part_ml; p.part_o = s.part_o;
+  p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
+  p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
+  p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
+  p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
+  p.v_sb = a.v_stride_b; p.v_st = a.v_stride_t; p.v_sh = a.v_stride_h;
+  p.t_new = static_cast<int32_t>(a.t_new);
+  p.t_max = static_cast<int32_t>(a.t_max);
+  p.n_heads = static_cast<int32_t>(a.n_heads);
+  p.n_kv_heads = static_cast<int32_t>(a.n_kv_heads);
+  p.group = plan.group;
+  p.n_hblocks = plan.n_hblocks;
+  p.window = a.window_left;
+  p.scale_log2 = a.softmax_scale * 1.4426950408889634f;
+  p.q_dtype = a.q_dtype;
+  p.num_splits = plan.num_splits;
+  p.keys_per_split = plan.keys_per_split;
+  p.fused = fused_append ? 1 : 0;
+  const bool qpk = a.q_dtype == a.cache_dtype && a.cache_dtype != NC_DTYPE_F32;
+  switch (a.cache_dtype) {
+    case NC_DTYPE_BF16:
+      return qpk ? launch_dt<bf16, true>(p, a.head_dim, plan.head_block, plan.n_wg, stream)
+                 : launch_dt<bf16, false>(p, a.head_dim, plan.head_block, plan.n_wg, stream);
+    case NC_DTYPE_F16:
+      return qpk ? launch_dt<f16, true>(p, a.head_dim, plan.head_block, plan.n_wg, stream)
+                 : launch_dt<f16, false>(p, a.head_dim, plan.head_block, plan.n_wg, stream);
+    default:
+      return launch_dt<float, false>(p, a.head_dim, plan.head_block, plan.n_wg, stream);
+  }
+}
+
+}  // namespace nckv

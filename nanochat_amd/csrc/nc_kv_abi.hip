@@ -1,0 +1,211 @@
+// C ABI entry points of libnc_kv.so: argument validation, launch planning and
+// dispatch.  Nothing here allocates, synchronises or keeps mutable state.
+
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "nc_kv.h"
+#include "nc_kv_internal.hpp"
+
+namespace nckv {
+
+int split_weight_capacity(int64_t head_dim);
+
+namespace {
+
+constexpr int kMaxSplits = 256;
+
+bool valid_dtype(int d) { return d == NC_DTYPE_F32 || d == NC_DTYPE_F16 || d == NC_DTYPE_BF16; }
+int64_t dtype_bytes(int d) { return d == NC_DTYPE_F32 ? 4 : 2; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool strides16(int64_t ebytes, int64_t s0, int64_t s1, int64_t s2) {
+  return (s0 * ebytes) % 16 == 0 && (s1 * ebytes) % 16 == 0 && (s2 * ebytes) % 16 == 0;
+}
+size_t round256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+}  // namespace
+
+int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
+  if (a.batch <= 0 || a.t_new <= 0 || a.t_max <= 0 || a.n_heads <= 0 || a.n_kv_heads <= 0 ||
+      a.head_dim <= 0) {
+    return NC_ERR_BAD_SHAPE;
+  }
+  if (a.n_heads % a.n_kv_heads != 0) return NC_ERR_BAD_SHAPE;
+  if (a.t_max > INT32_MAX / 2 || a.t_new > INT32_MAX / 2) return NC_ERR_BAD_SHAPE;
+  if (!valid_dtype(a.q_dtype) || !valid_dtype(a.cache_dtype)) return NC_ERR_DTYPE;
+  if (!decode_supports(a.cache_dtype, a.head_dim)) return NC_ERR_HEAD_DIM;
+  if (a.keys_per_split < 0 || a.keys_per_split % 64 != 0) return NC_ERR_BAD_SHAPE;
+
+  const int group = static_cast<int>(a.n_heads / a.n_kv_heads);
+  int hb = 1;
+  for (int c : {8, 4, 2}) {
+    if (group % c == 0) { hb = c; break; }
+  }
+  plan->group = group;
+  plan->head_block = hb;
+  plan->n_hblocks = group / hb;
+
+  const int64_t ebytes = dtype_bytes(a.cache_dtype);
+  const int64_t max_keys = a.window_left >= 0 ? std::min<int64_t>(a.t_max, int64_t(a.window_left) + 1) : a.t_max;
+  int64_t kps = a.keys_per_split;
+  if (kps == 0) {
+    // ~64 KiB of K (and as much V) per workgroup.
+    kps = std::max<int64_t>(64, (65536 / (a.head_dim * ebytes)) / 64 * 64);
+  }
+  const int64_t cap = std::min<int64_t>(kMaxSplits, split_weight_capacity(a.head_dim));
+  int64_t ns = (max_keys + kps - 1) / kps;
+  if (ns > cap) {
+    kps = ((max_keys + cap - 1) / cap + 63) / 64 * 64;
+    ns = (max_keys + kps - 1) / kps;
+  }
+  plan->keys_per_split = static_cast<int>(kps);
+  plan->num_splits = static_cast<int>(ns);
+  plan->n_wg = a.batch * a.t_new * a.n_kv_heads * plan->n_hblocks * ns;
+  if (plan->n_wg <= 0 || plan->n_wg > INT32_MAX) return NC_ERR_BAD_SHAPE;
+
+  if (ns > 1) {
+    const size_t pairs = static_cast<size_t>(a.batch * a.t_new * a.n_heads);
+    plan->counters_bytes = round256(static_cast<size_t>(a.batch * a.t_new * a.n_kv_heads * plan->n_hblocks) * 4);
+    plan->ml_bytes = round256(pairs * ns * 2 * 4);
+    plan->o_bytes = round256(pairs * ns * static_cast<size_t>(a.head_dim) * 4);
+  } else {
+    plan->counters_bytes = plan->ml_bytes = plan->o_bytes = 0;
+  }
+  plan->total_bytes = plan->counters_bytes + plan->ml_bytes + plan->o_bytes;
+  return NC_OK;
+}
+
+}  // namespace nckv
+
+using namespace nckv;
+
+extern "C" {
+
+int nc_abi_version(void) { return NC_KV_ABI_VERSION; }
+
+int nc_supports_head_dim(int64_t head_dim) { return decode_supports(NC_DTYPE_BF16, head_dim) ? 1 : 0; }
+
+const char* nc_strerror(int status) {
+  switch (status) {
+    case NC_OK: return "ok";
+    case NC_ERR_NULL_ARG: return "a required pointer argument is NULL";
+    case NC_ERR_BAD_SHAPE: return "invalid or inconsistent sizes";
+    case NC_ERR_DTYPE: return "unsupported dtype combination";
+    case NC_ERR_HEAD_DIM: return "head_dim not supported by the compiled kernels (32, 64, 128, 256)";
+    case NC_ERR_ALIGNMENT: return "pointer or stride not 16-byte aligned";
+    case NC_ERR_WORKSPACE: return "workspace missing or too small";
+    case NC_ERR_LAUNCH: return "kernel launch failed";
+    default: return "unknown nc_status";
+  }
+}
+
+int nc_kv_append(const nc_append_args* args, void* stream) {
+  if (args == nullptr) return NC_ERR_NULL_ARG;
+  const nc_append_args& a = *args;
+  if (!a.k_cache || !a.v_cache || !a.k || !a.v || !a.cache_seqlens) return NC_ERR_NULL_ARG;
+  if (a.batch <= 0 || a.t_new <= 0 || a.t_max <= 0 || a.n_kv_heads <= 0 || a.head_dim <= 0) {
+    return NC_ERR_BAD_SHAPE;
+  }
+  if (!valid_dtype(a.in_dtype) || !valid_dtype(a.cache_dtype)) return NC_ERR_DTYPE;
+  const int64_t eb = dtype_bytes(a.cache_dtype);
+  if ((a.head_dim * eb) % 16 != 0) return NC_ERR_HEAD_DIM;
+  if (!aligned16(a.k_cache) || !aligned16(a.v_cache) ||
+      !strides16(eb, a.kc_stride_b, a.kc_stride_t, a.kc_stride_h) ||
+      !strides16(eb, a.vc_stride_b, a.vc_stride_t, a.vc_stride_h)) {
+    return NC_ERR_ALIGNMENT;
+  }
+  if (a.in_dtype == a.cache_dtype &&
+      (!aligned16(a.k) || !aligned16(a.v) || !strides16(eb, a.k_stride_b, a.k_stride_t, a.k_stride_h) ||
+       !strides16(eb, a.v_stride_b, a.v_stride_t, a.v_stride_h))) {
+    return NC_ERR_ALIGNMENT;
+  }
+  return launch_append(a, static_cast<hipStream_t>(stream)) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
+}
+
+int nc_kv_fanout(const nc_fanout_args* args, void* stream) {
+  if (args == nullptr) return NC_ERR_NULL_ARG;
+  const nc_fanout_args& a = *args;
+  if (!a.k_src || !a.v_src || !a.k_dst || !a.v_dst) return NC_ERR_NULL_ARG;
+  if (a.n_layers <= 0 || a.n_rows <= 0 || a.prefix_len < 0 || a.row_elems <= 0) return NC_ERR_BAD_SHAPE;
+  if (a.n_layers > 65535 || a.n_rows > INT32_MAX || a.prefix_len > INT32_MAX) return NC_ERR_BAD_SHAPE;
+  if (!valid_dtype(a.dtype)) return NC_ERR_DTYPE;
+  const int64_t eb = dtype_bytes(a.dtype);
+  const int64_t region = a.prefix_len * a.row_elems * eb;
+  const uintptr_t ptr_or = reinterpret_cast<uintptr_t>(a.k_src) | reinterpret_cast<uintptr_t>(a.v_src) |
+                           reinterpret_cast<uintptr_t>(a.k_dst) | reinterpret_cast<uintptr_t>(a.v_dst);
+  const int64_t size_or = region | (a.src_stride_l * eb) | (a.dst_stride_l * eb) | (a.dst_stride_b * eb);
+  int unit = 2;
+  if ((ptr_or & 15u) == 0 && (size_or & 15) == 0) {
+    unit = 16;
+  } else if ((ptr_or & 3u) == 0 && (size_or & 3) == 0) {
+    unit = 4;
+  }
+  return launch_fanout(a, unit, static_cast<hipStream_t>(stream)) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
+}
+
+size_t nc_attn_workspace_bytes(const nc_attn_args* args) {
+  if (args == nullptr) return 0;
+  AttnPlan plan;
+  if (plan_attention(*args, &plan) != NC_OK) return 0;
+  return plan.total_bytes;
+}
+
+int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
+  if (args == nullptr) return NC_ERR_NULL_ARG;
+  const nc_attn_args& a = *args;
+  if (!a.q || !a.out || !a.k_cache || !a.v_cache || !a.cache_seqlens) return NC_ERR_NULL_ARG;
+  if ((a.k == nullptr) != (a.v == nullptr)) return NC_ERR_NULL_ARG;
+  AttnPlan plan;
+  const int st = plan_attention(a, &plan);
+  if (st != NC_OK) return st;
+
+  const int64_t eb = dtype_bytes(a.cache_dtype);
+  if (!aligned16(a.k_cache) || !aligned16(a.v_cache) ||
+      !strides16(eb, a.kc_stride_b, a.kc_stride_t, a.kc_stride_h) ||
+      !strides16(eb, a.vc_stride_b, a.vc_stride_t, a.vc_stride_h)) {
+    return NC_ERR_ALIGNMENT;
+  }
+  const bool same = a.q_dtype == a.cache_dtype;
+  if (same && (!aligned16(a.q) || !strides16(eb, a.q_stride_b, a.q_stride_t, a.q_stride_h))) {
+    return NC_ERR_ALIGNMENT;
+  }
+  if (a.k != nullptr && same &&
+      (!aligned16(a.k) || !aligned16(a.v) || !strides16(eb, a.k_stride_b, a.k_stride_t, a.k_stride_h) ||
+       !strides16(eb, a.v_stride_b, a.v_stride_t, a.v_stride_h))) {
+    return NC_ERR_ALIGNMENT;
+  }
+  if (plan.total_bytes > 0 && (a.workspace == nullptr || a.workspace_bytes < plan.total_bytes ||
+                               !aligned16(a.workspace))) {
+    return NC_ERR_WORKSPACE;
+  }
+
+  AttnScratch s;
+  char* ws = static_cast<char*>(a.workspace);
+  s.counters = reinterpret_cast<int32_t*>(ws);
+  s.part_ml = reinterpret_cast<float*>(ws + plan.counters_bytes);
+  s.part_o = reinterpret_cast<float*>(ws + plan.counters_bytes + plan.ml_bytes);
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+
+  bool fused = false;
+  if (a.k != nullptr) {
+    if (a.t_new == 1) {
+      fused = true;
+    } else {
+      nc_append_args ap;
+      ap.k_cache = a.k_cache; ap.v_cache = a.v_cache; ap.k = a.k; ap.v = a.v;
+      ap.cache_seqlens = a.cache_seqlens; ap.error_flag = a.error_flag;
+      ap.batch = a.batch; ap.t_new = a.t_new; ap.t_max = a.t_max;
+      ap.n_kv_heads = a.n_kv_heads; ap.head_dim = a.head_dim;
+      ap.kc_stride_b = a.kc_stride_b; ap.kc_stride_t = a.kc_stride_t; ap.kc_stride_h = a.kc_stride_h;
+      ap.vc_stride_b = a.vc_stride_b; ap.vc_stride_t = a.vc_stride_t; ap.vc_stride_h = a.vc_stride_h;
+      ap.k_stride_b = a.k_stride_b; ap.k_stride_t = a.k_stride_t; ap.k_stride_h = a.k_stride_h;
+      ap.v_stride_b = a.v_stride_b; ap.v_stride_t = a.v_stride_t; ap.v_stride_h = a.v_stride_h;
+      ap.in_dtype = a.q_dtype; ap.cache_dtype = a.cache_dtype;
+      if (launch_append(ap, hs) != hipSuccess) return NC_ERR_LAUNCH;
+    }
+  }
+  return launch_decode(a, plan, s, fused, hs) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
+}
+
+}  // extern "C"

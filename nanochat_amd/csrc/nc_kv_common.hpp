@@ -1,0 +1,166 @@
+// Device-side helpers shared by the KV-cache kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nc_kv.h"
+
+namespace nckv {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Element types.  Each cache element type knows how many elements a 16-byte
+// vector holds and how to widen a 16-byte vector to fp32.
+// ---------------------------------------------------------------------------
+struct bf16 { uint16_t bits; };
+struct f16 { uint16_t bits; };
+
+template <typename T> struct elem;
+template <> struct elem<float> {
+  static constexpr int kBytes = 4;
+  static constexpr int kDtype = NC_DTYPE_F32;
+};
+template <> struct elem<f16> {
+  static constexpr int kBytes = 2;
+  static constexpr int kDtype = NC_DTYPE_F16;
+};
+template <> struct elem<bf16> {
+  static constexpr int kBytes = 2;
+  static constexpr int kDtype = NC_DTYPE_BF16;
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float half_bits_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// fp32 -> bf16, round to nearest even; NaN becomes the canonical quiet NaN
+// 0x7FC0.  This is the rounding torch's Tensor.to(torch.bfloat16) applies.
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Widen the 16-byte vector `w` holding elements of type T to fp32.
+template <typename T> struct widen;
+template <> struct widen<bf16> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void run(const uint4& w, float* o) {
+    o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x);
+    o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
+    o[4] = bf16_lo(w.z); o[5] = bf16_hi(w.z);
+    o[6] = bf16_lo(w.w); o[7] = bf16_hi(w.w);
+  }
+};
+template <> struct widen<f16> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void run(const uint4& w, float* o) {
+    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = half_bits_to_f32(static_cast<uint16_t>(v[i] & 0xffffu));
+      o[2 * i + 1] = half_bits_to_f32(static_cast<uint16_t>(v[i] >> 16));
+    }
+  }
+};
+template <> struct widen<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void run(const uint4& w, float* o) {
+    o[0] = __uint_as_float(w.x); o[1] = __uint_as_float(w.y);
+    o[2] = __uint_as_float(w.z); o[3] = __uint_as_float(w.w);
+  }
+};
+
+// Scalar load of element i of a tensor whose dtype is known only at run
+// time (q, k, v inputs; a handful of elements per workgroup).
+__device__ __forceinline__ float load_any(const void* p, int64_t i, int dtype) {
+  if (dtype == NC_DTYPE_BF16) {
+    const uint16_t b = static_cast<const uint16_t*>(p)[i];
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+  }
+  if (dtype == NC_DTYPE_F16) return half_bits_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ void store_any(void* p, int64_t i, int dtype, float x) {
+  if (dtype == NC_DTYPE_BF16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16_rne(x);
+  } else if (dtype == NC_DTYPE_F16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_f16_rne(x);
+  } else {
+    static_cast<float*>(p)[i] = x;
+  }
+}
+
+// Cache-element encoding of an fp32 value (the value torch's copy_ stores).
+template <typename T> struct narrow;
+template <> struct narrow<bf16> {
+  __device__ __forceinline__ static uint16_t run(float x) { return f32_to_bf16_rne(x); }
+};
+template <> struct narrow<f16> {
+  __device__ __forceinline__ static uint16_t run(float x) { return f32_to_f16_rne(x); }
+};
+
+// Convert VEC consecutive elements of a runtime-typed input into one 16-byte
+// vector of cache type T.  When the input dtype equals T the bits are copied
+// unchanged (a plain 16-byte load), which is what a same-dtype copy_ does.
+template <typename T>
+__device__ __forceinline__ uint4 load_as_cache_vec(const void* base, int64_t off, int in_dtype) {
+  if (in_dtype == elem<T>::kDtype) {
+    return *reinterpret_cast<const uint4*>(static_cast<const char*>(base) + off * elem<T>::kBytes);
+  }
+  if constexpr (elem<T>::kBytes == 4) {
+    uint4 r;
+    r.x = __float_as_uint(load_any(base, off + 0, in_dtype));
+    r.y = __float_as_uint(load_any(base, off + 1, in_dtype));
+    r.z = __float_as_uint(load_any(base, off + 2, in_dtype));
+    r.w = __float_as_uint(load_any(base, off + 3, in_dtype));
+    return r;
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = narrow<T>::run(load_any(base, off + 2 * i, in_dtype));
+      const uint32_t hi = narrow<T>::run(load_any(base, off + 2 * i + 1, in_dtype));
+      w[i] = lo | (hi << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane sums inside groups of N consecutive lanes (N a power of two,
+// N <= 64).  N <= 16 stays inside a DPP row: quad_perm swaps for 1 and 2,
+// row_half_mirror for 4, row_mirror for 8.  Each step pairs lanes that already
+// hold equal partial sums, so the result is an all-reduce over the group.
+// ---------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "group size");
+  if constexpr (N >= 2) x += dpp_move<0xB1>(x);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) x += dpp_move<0x4E>(x);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) x += dpp_move<0x141>(x);  // row_half_mirror
+  if constexpr (N >= 16) x += dpp_move<0x140>(x); // row_mirror
+  if constexpr (N >= 32) x += __shfl_xor(x, 16, kWave);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32, kWave);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace nckv

@@ -1,0 +1,40 @@
+// Host-side launch interfaces between the C ABI (nc_kv_abi.hip) and the
+// kernel translation units.  Arguments have been validated by the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nc_kv.h"
+
+namespace nckv {
+
+// Split-K scratch carved out of the caller's workspace.
+struct AttnScratch {
+  int32_t* counters;   // one per (row, query, kv head, head block); zero between calls
+  float* part_ml;      // (pair, split, 2): running max (log2 domain) and sum
+  float* part_o;       // (pair, split, D): unnormalised output
+};
+
+// Launch plan shared by nc_attn_workspace_bytes and nc_attn_kvcache.
+struct AttnPlan {
+  int group;           // q heads per kv head
+  int head_block;      // q heads one workgroup handles (divides group)
+  int n_hblocks;       // group / head_block
+  int keys_per_split;
+  int num_splits;
+  int64_t n_wg;
+  size_t counters_bytes, ml_bytes, o_bytes, total_bytes;
+};
+
+// Returns NC_OK and fills `plan`, or an error code.
+int plan_attention(const nc_attn_args& a, AttnPlan* plan);
+
+hipError_t launch_append(const nc_append_args& a, hipStream_t stream);
+hipError_t launch_fanout(const nc_fanout_args& a, int unit_bytes, hipStream_t stream);
+hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
+                         bool fused_append, hipStream_t stream);
+
+bool decode_supports(int cache_dtype, int64_t head_dim);
+
+}  // namespace nckv

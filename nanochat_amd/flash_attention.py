@@ -1,0 +1,191 @@
+"""Drop-in for ``nanochat.flash_attention`` backed by gfx950 HIP kernels.
+
+Same public surface as nanochat/flash_attention.py:
+  - ``flash_attn`` namespace with ``flash_attn_with_kvcache`` and
+    ``flash_attn_func`` (nanochat/flash_attention.py:184-187);
+  - the module globals ``HAS_FA3``, ``USE_FA3``, ``_override_impl`` and
+    ``_resolve_use_fa3`` that nanochat's tests flip (:41-63).  There is no FA3
+    on MI355X and no SDPA fallback here: every call runs libnc_kv.so.
+
+Semantics of ``flash_attn_with_kvcache`` (nanochat/flash_attention.py:131-177):
+  - k/v (if given) are written in place into k_cache/v_cache at each row's own
+    position ``cache_seqlens[b]`` (FA3's contract; the reference fallback uses
+    row 0's position for all rows, :157, which is the same for uniform batches);
+  - cache_seqlens is read, never advanced (the caller advances, gpt.py:119-121);
+  - query i of row b sits at absolute position s_b + i (bottom-right aligned,
+    :94) and sees keys j <= s_b + i with s_b + i - j <= window_size[0] when
+    window_size[0] >= 0 (:96-100, :84-88);
+  - ``causal`` and ``window_size[1]`` are accepted and, as in the fallback,
+    do not change the mask;
+  - GQA maps q head h to kv head h // (H / H_kv) (SDPA enable_gqa, :174);
+  - the result is a new (B, T_new, H, D) tensor in q's dtype; k/v are stored
+    in the cache dtype with round-to-nearest-even; scores and sums are fp32.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from types import SimpleNamespace
+
+import torch
+
+from . import _ext
+
+# FA3 is a Hopper-only binary (nanochat/flash_attention.py:23-38); it does not
+# exist on MI355X.  The names stay so callers and tests that read them work.
+HAS_FA3 = False
+_override_impl = None
+
+_CHECK_ERRORS = os.environ.get("NANOCHAT_AMD_CHECK", "0") == "1"
+
+
+def _resolve_use_fa3():
+    """Mirror of nanochat/flash_attention.py:48-61: always False on MI355X."""
+    if _override_impl == 'fa3':
+        assert HAS_FA3, "Cannot override to FA3: not available on this hardware"
+        return True
+    return False
+
+
+USE_FA3 = _resolve_use_fa3()
+
+
+def _require_gpu(name: str, *tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(f"{name}: the MI355X KV-cache path runs on the GPU only (got device {dev})")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise ValueError(f"{name}: all tensors must be on {dev}, got {t.device}")
+    return dev
+
+
+def _dtype_code(t: torch.Tensor, name: str) -> int:
+    code = _ext.DTYPE_CODE.get(t.dtype)
+    if code is None:
+        raise TypeError(f"{name} has unsupported dtype {t.dtype} (float32, float16, bfloat16)")
+    return code
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
+                            causal=False, window_size=(-1, -1), *, keys_per_split: int = 0):
+    """Append k/v into the cache in place, then attend (see the module docstring).
+
+    q: (B, T_new, H, D); k_cache, v_cache: (B, T_max, H_kv, D);
+    k, v: (B, T_new, H_kv, D) or None; cache_seqlens: (B,) int32 on the GPU.
+    Returns (B, T_new, H, D) in q's dtype.
+    """
+    if cache_seqlens is None:
+        raise ValueError("flash_attn_with_kvcache: cache_seqlens is required")
+    if (k is None) != (v is None):
+        raise ValueError("flash_attn_with_kvcache: pass both k and v, or neither")
+    if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError("flash_attn_with_kvcache: q, k_cache, v_cache must be 4-D (B, T, H, D)")
+    B, T_new, H, D = q.shape
+    Bc, T_max, H_kv, Dc = k_cache.shape
+    if tuple(v_cache.shape) != (Bc, T_max, H_kv, Dc):
+        raise ValueError(f"v_cache shape {tuple(v_cache.shape)} != k_cache shape {tuple(k_cache.shape)}")
+    if Bc != B or Dc != D:
+        raise ValueError(f"cache shape {tuple(k_cache.shape)} does not match q shape {tuple(q.shape)}")
+    if H % H_kv != 0:
+        raise ValueError(f"n_heads {H} is not a multiple of n_kv_heads {H_kv}")
+    if k is not None:
+        if tuple(k.shape) != (B, T_new, H_kv, D) or tuple(v.shape) != (B, T_new, H_kv, D):
+            raise ValueError(f"k/v must have shape {(B, T_new, H_kv, D)}, got {tuple(k.shape)}, {tuple(v.shape)}")
+        if k.dtype != q.dtype or v.dtype != q.dtype:
+            raise TypeError(f"k/v dtype ({k.dtype}, {v.dtype}) must equal q dtype {q.dtype}")
+    if tuple(cache_seqlens.shape) != (B,) or cache_seqlens.dtype != torch.int32:
+        raise ValueError("cache_seqlens must be a (B,) int32 tensor")
+    if k_cache.dtype != v_cache.dtype:
+        raise TypeError("k_cache and v_cache must have the same dtype")
+    tensors = [q, k_cache, v_cache, cache_seqlens] + ([k, v] if k is not None else [])
+    dev = _require_gpu("flash_attn_with_kvcache", *tensors)
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("k", k), ("v", v)):
+        if t is not None and t.stride(-1) != 1:
+            raise ValueError(f"{name} must be contiguous in its last (head_dim) dimension")
+    if not cache_seqlens.is_contiguous():
+        cache_seqlens = cache_seqlens.contiguous()
+
+    L = _ext.lib()
+    out = torch.empty((B, T_new, H, D), dtype=q.dtype, device=dev)
+    window = int(window_size[0]) if window_size is not None else -1
+    a = _ext.AttnArgs()
+    a.q = q.data_ptr(); a.out = out.data_ptr()
+    a.k_cache = k_cache.data_ptr(); a.v_cache = v_cache.data_ptr()
+    a.k = k.data_ptr() if k is not None else None
+    a.v = v.data_ptr() if v is not None else None
+    a.cache_seqlens = cache_seqlens.data_ptr()
+    a.error_flag = _ext.error_flag(dev).data_ptr()
+    a.batch, a.t_new, a.t_max = B, T_new, T_max
+    a.n_heads, a.n_kv_heads, a.head_dim = H, H_kv, D
+    a.q_stride_b, a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    a.kc_stride_b, a.kc_stride_t, a.kc_stride_h = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.vc_stride_b, a.vc_stride_t, a.vc_stride_h = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    if k is not None:
+        a.k_stride_b, a.k_stride_t, a.k_stride_h = k.stride(0), k.stride(1), k.stride(2)
+        a.v_stride_b, a.v_stride_t, a.v_stride_h = v.stride(0), v.stride(1), v.stride(2)
+    a.window_left = window if window >= 0 else -1
+    a.causal = 1 if causal else 0
+    a.softmax_scale = D ** -0.5
+    a.q_dtype = _dtype_code(q, "q")
+    a.cache_dtype = _dtype_code(k_cache, "k_cache")
+    a.keys_per_split = int(keys_per_split)
+    ref = ctypes.byref(a)
+    need = L.nc_attn_workspace_bytes(ref)
+    stream = _ext.stream_handle(dev)
+    ws = _ext.workspace(dev, stream, need)
+    if ws is not None:
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws.numel()
+    _ext.check(L.nc_attn_kvcache(ref, stream), "nc_attn_kvcache")
+    if _CHECK_ERRORS:
+        bits = _ext.read_and_clear_device_errors(dev)
+        if bits & _ext.NC_DEVERR_OVERFLOW:
+            raise RuntimeError("flash_attn_with_kvcache: cache_seqlens + T_new exceeds the cache length")
+    return out
+
+
+def flash_attn_func(q, k, v, causal=False, window_size=(-1, -1)):
+    """Forward-only attention without a cache (nanochat/flash_attention.py:107-128).
+
+    Runs the cache kernel with k/v as a filled cache and zero positions, which
+    is exactly the reference's causal/windowed mask.  Training (autograd) is
+    not part of this library.
+    """
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        raise NotImplementedError("flash_attn_func: backward is not implemented by the MI355X KV-cache library")
+    B = q.shape[0]
+    zeros = torch.zeros(B, dtype=torch.int32, device=q.device)
+    return flash_attn_with_kvcache(q, k, v, cache_seqlens=zeros, causal=causal, window_size=window_size)
+
+
+def kv_append(k_cache, v_cache, k, v, cache_seqlens):
+    """Standalone ragged append (the first half of flash_attn_with_kvcache)."""
+    B, T_new, H_kv, D = k.shape
+    _, T_max, _, _ = k_cache.shape
+    dev = _require_gpu("kv_append", k_cache, v_cache, k, v, cache_seqlens)
+    if tuple(v.shape) != tuple(k.shape) or tuple(v_cache.shape) != tuple(k_cache.shape):
+        raise ValueError("kv_append: k/v and k_cache/v_cache shapes must match")
+    if k_cache.shape[0] != B or k_cache.shape[2] != H_kv or k_cache.shape[3] != D:
+        raise ValueError("kv_append: k does not match the cache shape")
+    if k.dtype != v.dtype or k_cache.dtype != v_cache.dtype:
+        raise TypeError("kv_append: k/v dtypes and cache dtypes must match pairwise")
+    a = _ext.AppendArgs()
+    a.k_cache = k_cache.data_ptr(); a.v_cache = v_cache.data_ptr()
+    a.k = k.data_ptr(); a.v = v.data_ptr()
+    a.cache_seqlens = cache_seqlens.data_ptr()
+    a.error_flag = _ext.error_flag(dev).data_ptr()
+    a.batch, a.t_new, a.t_max, a.n_kv_heads, a.head_dim = B, T_new, T_max, H_kv, D
+    a.kc_stride_b, a.kc_stride_t, a.kc_stride_h = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    a.vc_stride_b, a.vc_stride_t, a.vc_stride_h = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    a.k_stride_b, a.k_stride_t, a.k_stride_h = k.stride(0), k.stride(1), k.stride(2)
+    a.v_stride_b, a.v_stride_t, a.v_stride_h = v.stride(0), v.stride(1), v.stride(2)
+    a.in_dtype = _dtype_code(k, "k")
+    a.cache_dtype = _dtype_code(k_cache, "k_cache")
+    _ext.check(_ext.lib().nc_kv_append(ctypes.byref(a), _ext.stream_handle(dev)), "nc_kv_append")
+
+
+flash_attn = SimpleNamespace(
+    flash_attn_func=flash_attn_func,
+    flash_attn_with_kvcache=flash_attn_with_kvcache,
+)

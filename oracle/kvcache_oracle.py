@@ -1,0 +1,171 @@
+"""CPU restatement of nanochat's inference KV-cache path -- TEST INFRASTRUCTURE.
+
+This module is the parity checker for the HIP library.  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg may import it, and
+only as the checker or as the timed CPU baseline; the product (nanochat_amd/)
+never imports it.
+
+It restates, with the same torch operations the reference uses:
+  - _sdpa_attention            nanochat/flash_attention.py:69-102
+  - flash_attn_with_kvcache    nanochat/flash_attention.py:155-177, applied row
+                               by row with each row's own cache_seqlens[b] (FA3's
+                               per-row contract, nanochat/engine.py:84-90); for a
+                               uniform batch this is the reference fallback itself
+  - KVCache                    nanochat/engine.py:82-137
+  - compute_window_sizes       nanochat/gpt.py:285-312
+The pins for each function (brute force, closed forms, the reference's own
+known-answer test) live in tests/test_oracle.py.
+
+Mixed dtypes (F7 of the path analysis: fp32 compute with a bf16 cache on the
+GPU) are defined as: k/v are rounded into the cache dtype on store (torch
+copy_ semantics), the cache is upcast to q's dtype for attention, and the
+output has q's dtype.  ``compute_dtype`` lets a test run the same algorithm
+in float32 or float64 as the high-precision reference.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+
+def sdpa_attention(q, k, v, window_size, enable_gqa):
+    """nanochat/flash_attention.py:69-102.  q, k, v are (B, H, T, D)."""
+    Tq = q.size(2)
+    Tk = k.size(2)
+    window = window_size[0]
+    # :78-80 full context, same length
+    if (window < 0 or window >= Tq) and Tq == Tk:
+        return F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=enable_gqa)
+    # :82-89 single query: keep the last window+1 keys
+    if Tq == 1:
+        if 0 <= window < Tk:
+            start = max(0, Tk - (window + 1))
+            k = k[:, :, start:, :]
+            v = v[:, :, start:, :]
+        return F.scaled_dot_product_attention(q, k, v, is_causal=False, enable_gqa=enable_gqa)
+    # :91-102 explicit bottom-right aligned causal (+ window) mask
+    row_idx = (Tk - Tq) + torch.arange(Tq, device=q.device).unsqueeze(1)
+    col_idx = torch.arange(Tk, device=q.device).unsqueeze(0)
+    mask = col_idx <= row_idx
+    if 0 <= window < Tk:
+        mask = mask & ((row_idx - col_idx) <= window)
+    return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=enable_gqa)
+
+
+def kv_append(k_cache, v_cache, k, v, cache_seqlens):
+    """In-place append at each row's position: nanochat/flash_attention.py:160-162 per row."""
+    T_new = k.size(1)
+    for b in range(k.size(0)):
+        pos = int(cache_seqlens[b])
+        k_cache[b, pos:pos + T_new, :, :] = k[b]
+        v_cache[b, pos:pos + T_new, :, :] = v[b]
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
+                            causal=False, window_size=(-1, -1), compute_dtype=None):
+    """nanochat/flash_attention.py:155-177, one batch row at a time.
+
+    Mutates k_cache/v_cache like the reference.  ``compute_dtype`` (default:
+    q's dtype) is the dtype q and the cache slices are cast to before SDPA;
+    the result is returned in q's dtype.
+    """
+    B, T_new, H, D = q.shape
+    cdt = compute_dtype if compute_dtype is not None else q.dtype
+    outs = []
+    for b in range(B):
+        pos = int(cache_seqlens[b])
+        if k is not None and v is not None:
+            k_cache[b:b + 1, pos:pos + T_new, :, :] = k[b:b + 1]
+            v_cache[b:b + 1, pos:pos + T_new, :, :] = v[b:b + 1]
+        end_pos = pos + T_new
+        k_full = k_cache[b:b + 1, :end_pos, :, :].to(cdt)
+        v_full = v_cache[b:b + 1, :end_pos, :, :].to(cdt)
+        q_sdpa = q[b:b + 1].to(cdt).transpose(1, 2)
+        k_sdpa = k_full.transpose(1, 2)
+        v_sdpa = v_full.transpose(1, 2)
+        enable_gqa = q_sdpa.size(1) != k_sdpa.size(1)
+        y = sdpa_attention(q_sdpa, k_sdpa, v_sdpa, window_size, enable_gqa)
+        outs.append(y.transpose(1, 2))
+    return torch.cat(outs, dim=0).to(q.dtype)
+
+
+class KVCache:
+    """nanochat/engine.py:82-137 (CPU or any torch device)."""
+
+    def __init__(self, batch_size, num_heads, seq_len, head_dim, num_layers, device, dtype):
+        self.batch_size = batch_size
+        self.max_seq_len = seq_len
+        self.n_layers = num_layers
+        self.n_heads = num_heads
+        self.head_dim = head_dim
+        self.k_cache = torch.zeros(num_layers, batch_size, seq_len, num_heads, head_dim, device=device, dtype=dtype)
+        self.v_cache = torch.zeros(num_layers, batch_size, seq_len, num_heads, head_dim, device=device, dtype=dtype)
+        self.cache_seqlens = torch.zeros(batch_size, dtype=torch.int32, device=device)
+        self.prev_embedding = None
+
+    def reset(self):
+        self.cache_seqlens.zero_()
+        self.prev_embedding = None
+
+    def get_pos(self):
+        return self.cache_seqlens[0].item()
+
+    def get_layer_cache(self, layer_idx):
+        return self.k_cache[layer_idx], self.v_cache[layer_idx]
+
+    def advance(self, num_tokens):
+        self.cache_seqlens += num_tokens
+
+    def prefill(self, other):
+        assert self.get_pos() == 0, "Cannot prefill a non-empty KV cache"
+        assert self.n_layers == other.n_layers and self.n_heads == other.n_heads and self.head_dim == other.head_dim
+        assert self.max_seq_len >= other.max_seq_len
+        other_pos = other.get_pos()
+        self.k_cache[:, :, :other_pos, :, :] = other.k_cache[:, :, :other_pos, :, :]
+        self.v_cache[:, :, :other_pos, :, :] = other.v_cache[:, :, :other_pos, :, :]
+        self.cache_seqlens.fill_(other_pos)
+        if other.prev_embedding is not None:
+            self.prev_embedding = other.prev_embedding.expand(self.batch_size, -1, -1).clone()
+
+
+def kv_fanout(dst_k, dst_v, src_k, src_v, prefix_len):
+    """The broadcast copy of nanochat/engine.py:132-133 on (L, B, T, H, D) slabs."""
+    dst_k[:, :, :prefix_len, :, :] = src_k[:, :, :prefix_len, :, :]
+    dst_v[:, :, :prefix_len, :, :] = src_v[:, :, :prefix_len, :, :]
+
+
+def compute_window_sizes(sequence_len, window_pattern, n_layer):
+    """nanochat/gpt.py:285-312: per-layer (left, right) windows, last layer long."""
+    pattern = window_pattern.upper()
+    assert all(c in "SL" for c in pattern), f"Invalid window_pattern: {pattern}. Use only S and L."
+    long_window = sequence_len
+    short_window = -(-long_window // 4 // 128) * 128
+    char_to_window = {"L": (long_window, 0), "S": (short_window, 0)}
+    sizes = [char_to_window[pattern[i % len(pattern)]] for i in range(n_layer)]
+    sizes[-1] = (long_window, 0)
+    return sizes
+
+
+def decode_bytes(seqlens, n_layers, n_heads, n_kv_heads, head_dim, elem_bytes, windows=None):
+    """Algorithmic HBM bytes of one decode step (T_new = 1) over all layers.
+
+    Per layer and row: K and V of n_keys cached/new tokens read once, the new
+    K and V token written once, q read and the output written once, with
+    n_keys = min(s_b + 1, w + 1) (w < 0: s_b + 1).
+    """
+    total = 0
+    kv_tok = 2 * n_kv_heads * head_dim * elem_bytes
+    qo = 2 * n_heads * head_dim * elem_bytes
+    for layer in range(n_layers):
+        w = -1 if windows is None else windows[layer]
+        for s in seqlens:
+            s = int(s)
+            n_keys = s + 1 if w < 0 else min(s + 1, w + 1)
+            total += kv_tok * n_keys + kv_tok + qo
+    return total
+
+
+def softmax_scale(head_dim):
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,180 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/nc_kv.h declares, and its host-side validation and planning behave.
+(No kernel is launched here.)"""
+import ctypes
+import re
+
+import pytest
+import torch
+
+from nanochat_amd import _ext
+from tests.conftest import ROOT
+
+HEADER = ROOT / "include" / "nc_kv.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(nc_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    assert _declared_functions() == sorted(_ext.EXPORTS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _ext.lib()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.nc_abi_version() == _ext.ABI_VERSION
+
+
+def test_struct_layouts_match_header_field_order():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    for cname, pystruct in (("nc_append_args", _ext.AppendArgs), ("nc_fanout_args", _ext.FanoutArgs),
+                            ("nc_attn_args", _ext.AttnArgs)):
+        body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), text, flags=re.S).group(1)
+        names = []
+        for decl in body.split(";"):
+            decl = decl.strip()
+            if not decl:
+                continue
+            decl = re.sub(r"^(const\s+)?[\w]+\s*\*?\s*", "", decl)
+            names += [n.strip().lstrip("*") for n in decl.split(",")]
+        assert names == [f[0] for f in pystruct._fields_], cname
+
+
+def test_strerror_names_every_status():
+    lib = _ext.lib()
+    for code in range(8):
+        assert lib.nc_strerror(code).decode()
+    assert lib.nc_strerror(0).decode() == "ok"
+    assert lib.nc_strerror(99).decode() == "unknown nc_status"
+
+
+def test_supported_head_dims():
+    lib = _ext.lib()
+    assert [d for d in (16, 32, 64, 96, 128, 256) if lib.nc_supports_head_dim(d)] == [32, 64, 128, 256]
+
+
+def _attn_args(B=32, T_new=1, T_max=2304, H=10, H_kv=10, D=128, window=-1, dtype=2, kps=0):
+    a = _ext.AttnArgs()
+    a.batch, a.t_new, a.t_max, a.n_heads, a.n_kv_heads, a.head_dim = B, T_new, T_max, H, H_kv, D
+    a.window_left = window
+    a.q_dtype = a.cache_dtype = dtype
+    a.keys_per_split = kps
+    a.softmax_scale = D ** -0.5
+    return a
+
+
+def test_workspace_plan_for_d20_decode():
+    lib = _ext.lib()
+    a = _attn_args()
+    # 2304 keys / 256 keys per split = 9 splits; counters + (m, l) + o partials
+    pairs = 32 * 10
+    expect = 256 * ((32 * 10 * 4 + 255) // 256) + 256 * ((pairs * 9 * 8 + 255) // 256) + pairs * 9 * 128 * 4
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(a)) == expect
+
+
+def test_workspace_zero_for_single_split_and_window_caps_keys():
+    lib = _ext.lib()
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=200))) == 0
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=4096, window=255))) == 0
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=4096, window=256))) > 0
+
+
+def test_invalid_arguments_are_rejected_before_launch():
+    lib = _ext.lib()
+    a = _attn_args()
+    assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 1  # NULL pointers
+    fake = 1 << 20
+    a.q = a.out = a.k_cache = a.v_cache = a.cache_seqlens = fake
+    a.n_kv_heads = 3
+    assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 2  # 10 % 3 != 0
+    a.n_kv_heads = 10
+    a.head_dim = 96
+    assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 4  # head_dim
+    a.head_dim = 128
+    a.cache_dtype = 7
+    assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 3  # dtype
+    a.cache_dtype = 2
+    a.kc_stride_t = 3  # 6 bytes: not 16-byte aligned
+    assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 5
+    a.kc_stride_t = a.vc_stride_t = 1280
+    a.q_stride_h = 128
+    a.workspace = None
+    assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 6  # 9 splits need a workspace
+    a.keys_per_split = 100
+    assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 2  # not a multiple of 64
+
+
+def test_fanout_and_append_reject_bad_arguments():
+    lib = _ext.lib()
+    f = _ext.FanoutArgs()
+    assert lib.nc_kv_fanout(ctypes.byref(f), None) == 1
+    f.k_src = f.v_src = f.k_dst = f.v_dst = 1 << 20
+    f.n_layers, f.n_rows, f.prefix_len, f.row_elems = 0, 1, 1, 1
+    assert lib.nc_kv_fanout(ctypes.byref(f), None) == 2
+    a = _ext.AppendArgs()
+    assert lib.nc_kv_append(ctypes.byref(a), None) == 1
+    a.k_cache = a.v_cache = a.k = a.v = a.cache_seqlens = 1 << 20
+    a.batch, a.t_new, a.t_max, a.n_kv_heads, a.head_dim = 1, 1, 4, 1, 5
+    a.cache_dtype = a.in_dtype = 2
+    assert lib.nc_kv_append(ctypes.byref(a), None) == 4  # 10-byte rows cannot be 16-byte vectors
+
+
+def test_python_surface_rejects_cpu_tensors_and_bad_shapes():
+    from nanochat_amd.flash_attention import flash_attn
+    q = torch.zeros(2, 1, 4, 32)
+    kc = torch.zeros(2, 8, 4, 32)
+    sl = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        flash_attn.flash_attn_with_kvcache(q, kc, kc.clone(), k=q, v=q, cache_seqlens=sl)
+    with pytest.raises(ValueError):
+        flash_attn.flash_attn_with_kvcache(q, kc[:, :, :3], kc[:, :, :3].clone(), cache_seqlens=sl)
+    with pytest.raises(ValueError):
+        flash_attn.flash_attn_with_kvcache(q, kc, kc.clone(), k=q, v=None, cache_seqlens=sl)
+    with pytest.raises(ValueError):
+        flash_attn.flash_attn_with_kvcache(q, kc, kc.clone(), cache_seqlens=sl.long())
+
+
+def test_override_mechanism_mirrors_reference():
+    """nanochat tests/test_attention_fallback.py:340-359 on this module."""
+    import nanochat_amd.flash_attention as fa
+    fa._override_impl = 'sdpa'
+    fa.USE_FA3 = fa._resolve_use_fa3()
+    assert fa.USE_FA3 is False
+    fa._override_impl = None
+    fa.USE_FA3 = fa._resolve_use_fa3()
+    assert fa.USE_FA3 == fa.HAS_FA3
+    fa._override_impl = 'fa3'
+    with pytest.raises(AssertionError):
+        fa._resolve_use_fa3()
+    fa._override_impl = None
+
+
+def test_kv_cache_basic_on_cpu():
+    """nanochat tests/test_engine.py:84-121 against nanochat_amd.KVCache."""
+    from nanochat_amd.engine import KVCache
+    c = KVCache(batch_size=2, num_heads=3, seq_len=64, head_dim=5, num_layers=6, device="cpu", dtype=torch.float32)
+    assert c.get_pos() == 0
+    assert c.k_cache.shape == (6, 2, 64, 3, 5) and c.v_cache.shape == (6, 2, 64, 3, 5)
+    c.advance(10)
+    assert c.get_pos() == 10
+    c.advance(5)
+    assert c.get_pos() == 15
+    c.reset()
+    assert c.get_pos() == 0
+    k0, v0 = c.get_layer_cache(0)
+    assert k0.shape == (2, 64, 3, 5) and v0.shape == (2, 64, 3, 5)
+    assert k0.data_ptr() == c.k_cache.data_ptr()  # views, not copies
+
+
+def test_prefill_on_cpu_fails_loudly():
+    from nanochat_amd.engine import KVCache
+    src = KVCache(1, 2, 8, 8, 1, "cpu", torch.float32)
+    src.advance(4)
+    dst = KVCache(2, 2, 8, 8, 1, "cpu", torch.float32)
+    with pytest.raises(RuntimeError, match="GPU"):
+        dst.prefill(src)

@@ -1,0 +1,206 @@
+"""GPU parity of flash_attn_with_kvcache (decode split-K and chunk paths).
+
+Reference: the oracle (nanochat/flash_attention.py:155-177 + :69-102 applied
+row by row) evaluated on the CPU in float32 from the same seeded inputs.
+Tolerances (written per test): bf16/fp16 caches max rel err <= 2e-2 and
+torch.allclose(atol=1e-2, rtol=1e-2) (nanochat tests/test_attention_fallback.py:39);
+fp32 caches 1e-4.  Cache contents after the call are compared bit-exactly.
+"""
+import pytest
+import torch
+
+from nanochat_amd import _ext
+from nanochat_amd.flash_attention import flash_attn
+from oracle import kvcache_oracle as orc
+from tests.helpers import bits, gen, max_rel_err, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _inputs(seed, B, T_new, H, H_kv, D, T_max, seqlens, q_dtype, cache_dtype):
+    g = gen(seed)
+    q = randn((B, T_new, H, D), g, q_dtype)
+    k = randn((B, T_new, H_kv, D), g, q_dtype)
+    v = randn((B, T_new, H_kv, D), g, q_dtype)
+    kc = torch.zeros(B, T_max, H_kv, D, dtype=cache_dtype)
+    vc = torch.zeros(B, T_max, H_kv, D, dtype=cache_dtype)
+    for b, s in enumerate(seqlens):
+        s = int(s)
+        kc[b, :s] = randn((s, H_kv, D), g, cache_dtype)
+        vc[b, :s] = randn((s, H_kv, D), g, cache_dtype)
+    return q, k, v, kc, vc, torch.as_tensor(seqlens, dtype=torch.int32)
+
+
+def _tol(q_dtype, cache_dtype):
+    if q_dtype == torch.float32 and cache_dtype == torch.float32:
+        return 1e-4, 1e-4
+    return 2e-2, 1e-2
+
+
+def _check(seed, B, T_new, H, H_kv, D, T_max, seqlens, window, q_dtype=torch.bfloat16,
+           cache_dtype=torch.bfloat16, kps=0, with_kv=True):
+    q, k, v, kc, vc, sl = _inputs(seed, B, T_new, H, H_kv, D, T_max, seqlens, q_dtype, cache_dtype)
+    kc_d, vc_d, sl_d = kc.to(DEV), vc.to(DEV), sl.to(DEV)
+    kk = k.to(DEV) if with_kv else None
+    vv = v.to(DEV) if with_kv else None
+    out = flash_attn.flash_attn_with_kvcache(q.to(DEV), kc_d, vc_d, k=kk, v=vv, cache_seqlens=sl_d, causal=True,
+                                             window_size=(window, 0), keys_per_split=kps)
+    ref = orc.flash_attn_with_kvcache(q, kc, vc, k=k if with_kv else None, v=v if with_kv else None,
+                                      cache_seqlens=sl, causal=True, window_size=(window, 0),
+                                      compute_dtype=torch.float32)
+    assert out.shape == (B, T_new, H, D) and out.dtype == q_dtype
+    rel_tol, atol = _tol(q_dtype, cache_dtype)
+    err = max_rel_err(out, ref.float())
+    assert err <= rel_tol, f"max rel err {err:.3e}"
+    assert torch.allclose(out.float().cpu(), ref.float(), atol=atol, rtol=atol)
+    assert torch.equal(bits(kc_d), bits(kc)), "k_cache bytes differ from the oracle"
+    assert torch.equal(bits(vc_d), bits(vc)), "v_cache bytes differ from the oracle"
+    assert torch.equal(sl_d.cpu(), sl), "cache_seqlens must not be modified"
+    return out
+
+
+# ---- nanochat tests/test_attention_fallback.py scenarios, re-expressed ----
+def test_reference_scenario_prefill_into_empty_cache():
+    _check(1, 2, 16, 4, 4, 32, 64, [0, 0], 64)
+
+
+def test_reference_scenario_single_token():
+    _check(2, 2, 1, 4, 4, 32, 64, [16, 16], 64)
+
+
+def test_reference_scenario_single_token_sliding_window():
+    _check(3, 2, 1, 4, 4, 32, 64, [32, 32], 8)
+
+
+def test_reference_scenario_sdpa_only_kvcache_flow():
+    """TestSDPAOnly.test_kvcache: prefill 16 then decode 1 through KVCache and advance."""
+    from nanochat_amd.engine import KVCache
+    B, T_max, H, D = 2, 64, 4, 32
+    cache = KVCache(batch_size=B, num_heads=H, seq_len=T_max, head_dim=D, num_layers=1, device=DEV,
+                    dtype=torch.bfloat16)
+    k_cache, v_cache = cache.get_layer_cache(0)
+    g = gen(4)
+    q, k, v = (randn((B, 16, H, D), g, torch.bfloat16).to(DEV) for _ in range(3))
+    y = flash_attn.flash_attn_with_kvcache(q, k_cache, v_cache, k=k, v=v, cache_seqlens=cache.cache_seqlens,
+                                           causal=True, window_size=(T_max, 0))
+    cache.advance(16)
+    assert y.shape == (B, 16, H, D) and cache.get_pos() == 16
+    q1, k1, v1 = (randn((B, 1, H, D), g, torch.bfloat16).to(DEV) for _ in range(3))
+    y1 = flash_attn.flash_attn_with_kvcache(q1, k_cache, v_cache, k=k1, v=v1, cache_seqlens=cache.cache_seqlens,
+                                            causal=True, window_size=(T_max, 0))
+    cache.advance(1)
+    assert y1.shape == (B, 1, H, D) and cache.get_pos() == 17
+    assert not torch.isnan(y).any() and not torch.isnan(y1).any()
+
+
+# ---- decode (T_new = 1) ----
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+def test_decode_head_dims(D):
+    _check(10 + D, 3, 1, 4, 4, D, 200, [0, 77, 199], -1, kps=64)
+
+
+@pytest.mark.parametrize("H,H_kv", [(4, 4), (8, 2), (16, 4), (12, 4), (6, 2), (16, 2), (24, 3)])
+def test_decode_gqa(H, H_kv):
+    _check(20 + H, 4, 1, H, H_kv, 128, 300, [5, 130, 299, 64], -1, kps=64)
+
+
+@pytest.mark.parametrize("window", [0, 1, 37, 128, 511])
+def test_decode_sliding_window_ragged(window):
+    _check(30 + window, 5, 1, 4, 2, 128, 700, [0, 3, 250, 600, 699], window, kps=64)
+
+
+@pytest.mark.parametrize("q_dtype,cache_dtype", [
+    (torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16), (torch.float32, torch.float32),
+    (torch.float32, torch.bfloat16), (torch.float16, torch.bfloat16), (torch.bfloat16, torch.float32),
+])
+def test_decode_dtypes(q_dtype, cache_dtype):
+    _check(40, 3, 1, 8, 4, 128, 400, [17, 256, 399], 100, q_dtype=q_dtype, cache_dtype=cache_dtype, kps=128)
+
+
+@pytest.mark.parametrize("kps", [0, 64, 128, 512])
+def test_decode_split_sizes_agree(kps):
+    _check(50, 6, 1, 10, 10, 128, 1100, [0, 1, 511, 512, 513, 1099], -1, kps=kps)
+
+
+def test_decode_without_new_kv_reads_cache_only():
+    _check(60, 3, 1, 4, 4, 64, 100, [10, 50, 98], -1, with_kv=False, kps=64)
+
+
+def test_decode_repeated_calls_reuse_workspace():
+    """The split tickets reset themselves: many calls in a row stay correct."""
+    for i in range(5):
+        _check(70 + i, 4, 1, 8, 8, 128, 600, [100 * (i + 1), 7, 599 - i, 300], -1, kps=64)
+
+
+def test_decode_d20_shapes_ragged_batch():
+    """C2 shapes at B = 32 with the library's default split (one layer)."""
+    g = gen(0)
+    seqlens = torch.randint(512, 2049, (32,), generator=g, dtype=torch.int32).tolist()
+    _check(80, 32, 1, 10, 10, 128, 2304, seqlens, -1)
+
+
+# ---- chunk (T_new > 1) ----
+@pytest.mark.parametrize("T_new", [2, 7, 33])
+def test_chunk_ragged_window_gqa(T_new):
+    _check(90 + T_new, 3, T_new, 8, 2, 64, 300, [0, 41, 300 - T_new], 50, kps=64)
+
+
+def test_chunk_full_causal_into_nonempty_cache():
+    _check(95, 2, 24, 6, 6, 128, 400, [100, 376], -1)
+
+
+def test_chunk_fp32_compute_bf16_cache():
+    _check(96, 2, 9, 4, 4, 128, 128, [0, 60], 20, q_dtype=torch.float32, cache_dtype=torch.bfloat16)
+
+
+def test_chunk_equals_sequential_decode_on_gpu():
+    """Incremental-equals-full invariant through the HIP path itself."""
+    q, k, v, kc, vc, sl = _inputs(97, 2, 12, 4, 2, 128, 200, [30, 111], torch.bfloat16, torch.bfloat16)
+    kc1, vc1 = kc.to(DEV), vc.to(DEV)
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    qd, kd, vd, sld = q.to(DEV), k.to(DEV), v.to(DEV), sl.to(DEV)
+    full = flash_attn.flash_attn_with_kvcache(qd, kc1, vc1, k=kd, v=vd, cache_seqlens=sld, window_size=(40, 0))
+    steps = []
+    pos = sld.clone()
+    for t in range(12):
+        steps.append(flash_attn.flash_attn_with_kvcache(qd[:, t:t + 1], kc2, vc2, k=kd[:, t:t + 1],
+                                                        v=vd[:, t:t + 1], cache_seqlens=pos, window_size=(40, 0)))
+        pos += 1
+    assert torch.equal(bits(kc1), bits(kc2)) and torch.equal(bits(vc1), bits(vc2))
+    assert max_rel_err(full, torch.cat(steps, dim=1)) <= 1e-2
+
+
+def test_flash_attn_func_forward_matches_oracle():
+    g = gen(98)
+    q, k, v = (randn((2, 40, 4, 64), g, torch.bfloat16) for _ in range(3))
+    with torch.no_grad():
+        out = flash_attn.flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV), causal=True, window_size=(9, 0))
+    ref = orc.sdpa_attention(q.float().transpose(1, 2), k.float().transpose(1, 2), v.float().transpose(1, 2),
+                             (9, 0), False).transpose(1, 2)
+    assert max_rel_err(out, ref) <= 2e-2
+
+
+# ---- error behaviour ----
+def test_overflow_sets_device_flag():
+    dev = torch.device(DEV, torch.cuda.current_device())
+    _ext.read_and_clear_device_errors(dev)
+    q, k, v, kc, vc, sl = _inputs(99, 2, 1, 4, 4, 64, 16, [3, 16], torch.bfloat16, torch.bfloat16)
+    kc_d = kc.to(DEV)
+    out = flash_attn.flash_attn_with_kvcache(q.to(DEV), kc_d, vc.to(DEV), k=k.to(DEV), v=v.to(DEV),
+                                             cache_seqlens=sl.to(DEV))
+    assert _ext.read_and_clear_device_errors(dev) & _ext.NC_DEVERR_OVERFLOW
+    assert torch.isfinite(out.float()).all()
+    assert torch.equal(bits(kc_d[1]), bits(kc[1])), "row past the end must not be written"
+
+
+def test_mismatched_dtypes_raise():
+    q = torch.zeros(1, 1, 4, 64, dtype=torch.bfloat16, device=DEV)
+    kc = torch.zeros(1, 8, 4, 64, dtype=torch.bfloat16, device=DEV)
+    sl = torch.zeros(1, dtype=torch.int32, device=DEV)
+    with pytest.raises(TypeError):
+        flash_attn.flash_attn_with_kvcache(q, kc, kc.clone(), k=q.float(), v=q.float(), cache_seqlens=sl)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        q2 = torch.zeros(1, 1, 4, 48, dtype=torch.bfloat16, device=DEV)
+        kc2 = torch.zeros(1, 8, 4, 48, dtype=torch.bfloat16, device=DEV)
+        flash_attn.flash_attn_with_kvcache(q2, kc2, kc2.clone(), cache_seqlens=sl)

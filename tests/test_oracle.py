@@ -1,0 +1,254 @@
+"""Pins of the CPU oracle (oracle/kvcache_oracle.py), CPU only.
+
+Every oracle function is checked against something that does not retype its
+formula: an fp64 key-by-key brute force, closed forms, the reference's own
+known-answer test (tests/test_engine.py:124-155 of nanochat), and invariants.
+A planted-mistake test shows the brute-force check catches an off-by-one.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kvcache_oracle as orc
+from tests.helpers import brute_attention, gen, randn
+
+
+def _case(seed, B, T_new, H, H_kv, D, T_max, seqlens, dtype=torch.float64):
+    g = gen(seed)
+    q = randn((B, T_new, H, D), g, dtype)
+    k = randn((B, T_new, H_kv, D), g, dtype)
+    v = randn((B, T_new, H_kv, D), g, dtype)
+    kc = torch.zeros(B, T_max, H_kv, D, dtype=dtype)
+    vc = torch.zeros(B, T_max, H_kv, D, dtype=dtype)
+    for b, s in enumerate(seqlens):
+        kc[b, :s] = randn((s, H_kv, D), g, dtype)
+        vc[b, :s] = randn((s, H_kv, D), g, dtype)
+    sl = torch.tensor(seqlens, dtype=torch.int32)
+    return q, k, v, kc, vc, sl
+
+
+CASES = [
+    # (B, T_new, H, H_kv, D, T_max, seqlens, window)
+    (2, 1, 4, 4, 8, 40, [16, 16], -1),          # decode, uniform
+    (3, 1, 4, 2, 8, 40, [0, 7, 31], -1),        # decode, ragged, GQA 2:1, empty row
+    (3, 1, 4, 4, 8, 40, [5, 20, 33], 8),        # decode, window < Tk
+    (2, 5, 6, 2, 8, 40, [0, 11], -1),           # chunk into empty and non-empty cache
+    (2, 5, 4, 4, 8, 40, [3, 17], 4),            # chunk with window
+    (1, 6, 4, 1, 8, 16, [0], 40),               # Tq == Tk, window >= Tq: plain causal branch
+    (1, 6, 2, 2, 8, 16, [0], 2),                # Tq == Tk, window < Tq: explicit mask branch
+]
+
+
+@pytest.mark.parametrize("B,T_new,H,H_kv,D,T_max,seqlens,window", CASES)
+def test_oracle_matches_fp64_brute_force(B, T_new, H, H_kv, D, T_max, seqlens, window):
+    q, k, v, kc, vc, sl = _case(1, B, T_new, H, H_kv, D, T_max, seqlens)
+    out = orc.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=sl, causal=True,
+                                      window_size=(window, 0))
+    ref = brute_attention(q.numpy(), kc.numpy(), vc.numpy(), seqlens, window)
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-10, atol=1e-10)
+
+
+def test_oracle_append_closed_form():
+    """Appended tokens land at [s_b, s_b + T_new) of their row; nothing else changes."""
+    B, T_new, H_kv, D, T_max = 3, 4, 2, 4, 16
+    seqlens = [0, 5, 12]
+    kc = torch.full((B, T_max, H_kv, D), -1.0)
+    vc = torch.full((B, T_max, H_kv, D), -2.0)
+    # code(b, t, h, d) makes every appended element distinct
+    code = torch.arange(B * T_new * H_kv * D, dtype=torch.float32).view(B, T_new, H_kv, D)
+    orc.kv_append(kc, vc, code, code + 1000, torch.tensor(seqlens, dtype=torch.int32))
+    for b in range(B):
+        for pos in range(T_max):
+            t = pos - seqlens[b]
+            if 0 <= t < T_new:
+                assert torch.equal(kc[b, pos], code[b, t])
+                assert torch.equal(vc[b, pos], code[b, t] + 1000)
+            else:
+                assert (kc[b, pos] == -1.0).all() and (vc[b, pos] == -2.0).all()
+
+
+def test_oracle_cache_written_by_attention_call():
+    q, k, v, kc, vc, sl = _case(2, 2, 3, 4, 2, 8, 20, [4, 9])
+    kc0, vc0 = kc.clone(), vc.clone()
+    orc.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=sl, window_size=(-1, 0))
+    for b, s in enumerate([4, 9]):
+        assert torch.equal(kc[b, s:s + 3], k[b]) and torch.equal(vc[b, s:s + 3], v[b])
+        assert torch.equal(kc[b, :s], kc0[b, :s]) and torch.equal(kc[b, s + 3:], kc0[b, s + 3:])
+    assert torch.equal(sl, torch.tensor([4, 9], dtype=torch.int32)), "cache_seqlens must not move"
+
+
+def test_single_key_returns_v_exactly():
+    """s = 0, T_new = 1: softmax over one key is 1, so the output is v itself."""
+    q, k, v, kc, vc, sl = _case(3, 2, 1, 4, 2, 8, 8, [0, 0], dtype=torch.float32)
+    out = orc.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=sl)
+    expect = v.repeat_interleave(2, dim=2)
+    assert torch.equal(out, expect)
+
+
+def test_constant_keys_average_values():
+    """All keys equal: the weights are uniform over the visible window."""
+    B, H, D, T_max, s, w = 1, 2, 8, 32, 20, 5
+    g = gen(4)
+    q = randn((B, 1, H, D), g, torch.float64)
+    kc = torch.ones(B, T_max, H, D, dtype=torch.float64)
+    vc = randn((B, T_max, H, D), g, torch.float64)
+    k = torch.ones(B, 1, H, D, dtype=torch.float64)
+    v = randn((B, 1, H, D), g, torch.float64)
+    out = orc.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=torch.tensor([s], dtype=torch.int32),
+                                      window_size=(w, 0))
+    expect = vc[0, s - w:s + 1].mean(dim=0)
+    torch.testing.assert_close(out[0, 0], expect, rtol=1e-12, atol=1e-12)
+
+
+def test_window_covering_everything_equals_full():
+    q, k, v, kc, vc, sl = _case(5, 2, 3, 4, 4, 8, 30, [10, 20])
+    a = orc.flash_attn_with_kvcache(q, kc.clone(), vc.clone(), k=k, v=v, cache_seqlens=sl, window_size=(-1, 0))
+    b = orc.flash_attn_with_kvcache(q, kc.clone(), vc.clone(), k=k, v=v, cache_seqlens=sl, window_size=(10_000, 0))
+    torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-12)
+
+
+def test_gqa_equals_repeated_mha():
+    q, k, v, kc, vc, sl = _case(6, 2, 2, 8, 2, 8, 24, [3, 15])
+    gqa = orc.flash_attn_with_kvcache(q, kc.clone(), vc.clone(), k=k, v=v, cache_seqlens=sl, window_size=(6, 0))
+    rep = lambda t: t.repeat_interleave(4, dim=2)
+    mha = orc.flash_attn_with_kvcache(q, rep(kc), rep(vc), k=rep(k), v=rep(v), cache_seqlens=sl, window_size=(6, 0))
+    torch.testing.assert_close(gqa, mha, rtol=1e-12, atol=1e-12)
+
+
+def test_chunk_equals_sequential_decode():
+    """Appending T tokens at once equals appending them one at a time."""
+    q, k, v, kc, vc, sl = _case(7, 2, 6, 4, 2, 8, 30, [4, 9])
+    kc2, vc2 = kc.clone(), vc.clone()
+    chunk = orc.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=sl, window_size=(5, 0))
+    steps = []
+    pos = sl.clone()
+    for t in range(6):
+        steps.append(orc.flash_attn_with_kvcache(q[:, t:t + 1], kc2, vc2, k=k[:, t:t + 1], v=v[:, t:t + 1],
+                                                 cache_seqlens=pos, window_size=(5, 0)))
+        pos = pos + 1
+    torch.testing.assert_close(chunk, torch.cat(steps, dim=1), rtol=1e-12, atol=1e-12)
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+
+
+def test_uniform_batch_matches_reference_fallback_shape_of_computation():
+    """For a uniform batch the row-by-row oracle equals one batched fallback call."""
+    q, k, v, kc, vc, sl = _case(8, 3, 4, 4, 2, 8, 24, [7, 7, 7])
+    per_row = orc.flash_attn_with_kvcache(q, kc.clone(), vc.clone(), k=k, v=v, cache_seqlens=sl,
+                                          window_size=(3, 0))
+    # the reference's batched form: one position for all rows (flash_attention.py:157-177)
+    kb, vb = kc.clone(), vc.clone()
+    kb[:, 7:11] = k
+    vb[:, 7:11] = v
+    y = orc.sdpa_attention(q.transpose(1, 2), kb[:, :11].transpose(1, 2), vb[:, :11].transpose(1, 2), (3, 0), True)
+    torch.testing.assert_close(per_row, y.transpose(1, 2), rtol=1e-12, atol=1e-12)
+
+
+def test_mixed_dtype_rounds_on_store():
+    """fp32 k/v into a bf16 cache: stored values are torch's RNE casts."""
+    q, k, v, kc, vc, sl = _case(9, 2, 1, 2, 2, 8, 8, [2, 5], dtype=torch.float32)
+    kcb, vcb = kc.to(torch.bfloat16), vc.to(torch.bfloat16)
+    orc.flash_attn_with_kvcache(q, kcb, vcb, k=k, v=v, cache_seqlens=sl)
+    assert torch.equal(kcb[0, 2], k[0, 0].to(torch.bfloat16))
+    assert torch.equal(vcb[1, 5], v[1, 0].to(torch.bfloat16))
+
+
+def test_brute_force_detects_planted_window_off_by_one(monkeypatch):
+    """Plant an off-by-one (window+2 keys) in the oracle; the brute-force pin must fail."""
+    orig = orc.sdpa_attention
+
+    def planted(q, k, v, window_size, enable_gqa):
+        w = window_size[0]
+        return orig(q, k, v, (w + 1 if w >= 0 else w, 0), enable_gqa)
+
+    monkeypatch.setattr(orc, "sdpa_attention", planted)
+    q, k, v, kc, vc, sl = _case(10, 2, 1, 4, 4, 8, 40, [20, 30])
+    out = orc.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=sl, window_size=(6, 0))
+    ref = brute_attention(q.numpy(), kc.numpy(), vc.numpy(), [20, 30], 6)
+    assert not np.allclose(out.numpy(), ref, rtol=1e-6, atol=1e-6)
+
+
+def test_brute_force_detects_planted_gqa_mapping(monkeypatch):
+    """Plant a wrong GQA head map (h -> h % H_kv instead of h // G); the pin must fail."""
+    orig = orc.sdpa_attention
+
+    def planted(q, k, v, window_size, enable_gqa):
+        if enable_gqa:
+            G = q.size(1) // k.size(1)
+            k, v = k.repeat(1, G, 1, 1), v.repeat(1, G, 1, 1)
+        return orig(q, k, v, window_size, False)
+
+    q, k, v, kc, vc, sl = _case(11, 1, 1, 4, 2, 8, 16, [9])
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    orc.kv_append(kc_ref, vc_ref, k, v, sl)
+    ref = brute_attention(q.numpy(), kc_ref.numpy(), vc_ref.numpy(), [9], -1)
+    good = orc.flash_attn_with_kvcache(q, kc.clone(), vc.clone(), k=k, v=v, cache_seqlens=sl)
+    np.testing.assert_allclose(good.numpy(), ref, rtol=1e-10, atol=1e-10)
+    monkeypatch.setattr(orc, "sdpa_attention", planted)
+    wrong = orc.flash_attn_with_kvcache(q, kc.clone(), vc.clone(), k=k, v=v, cache_seqlens=sl)
+    assert not np.allclose(wrong.numpy(), ref, rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# KVCache: nanochat's own tests (tests/test_engine.py:84-155) on the oracle cache
+# ---------------------------------------------------------------------------
+def test_oracle_kv_cache_basic():
+    c = orc.KVCache(batch_size=2, num_heads=3, seq_len=64, head_dim=5, num_layers=6, device="cpu", dtype=torch.float32)
+    assert c.get_pos() == 0
+    assert c.k_cache.shape == (6, 2, 64, 3, 5) and c.v_cache.shape == (6, 2, 64, 3, 5)
+    c.advance(10)
+    assert c.get_pos() == 10
+    c.advance(5)
+    assert c.get_pos() == 15
+    c.reset()
+    assert c.get_pos() == 0
+    k0, v0 = c.get_layer_cache(0)
+    assert k0.shape == (2, 64, 3, 5) and v0.shape == (2, 64, 3, 5)
+
+
+def test_oracle_kv_cache_prefill_known_answer():
+    """nanochat tests/test_engine.py:124-155: 1.0 / 2.0 fill copied through prefill."""
+    src = orc.KVCache(batch_size=1, num_heads=4, seq_len=32, head_dim=8, num_layers=2, device="cpu", dtype=torch.float32)
+    src.k_cache[0, 0, :16, :, :] = 1.0
+    src.v_cache[0, 0, :16, :, :] = 2.0
+    src.advance(16)
+    dst = orc.KVCache(batch_size=1, num_heads=4, seq_len=64, head_dim=8, num_layers=2, device="cpu", dtype=torch.float32)
+    dst.prefill(src)
+    assert dst.get_pos() == 16
+    assert (dst.k_cache[0, 0, :16] == 1.0).all() and (dst.v_cache[0, 0, :16] == 2.0).all()
+    assert (dst.k_cache[:, :, 16:] == 0).all() and (dst.k_cache[1] == 0).all()
+
+
+def test_oracle_prefill_preconditions():
+    a = orc.KVCache(1, 2, 8, 4, 1, "cpu", torch.float32)
+    b = orc.KVCache(1, 2, 4, 4, 1, "cpu", torch.float32)
+    with pytest.raises(AssertionError):
+        b.prefill(a)  # destination shorter than source
+    a.advance(1)
+    with pytest.raises(AssertionError):
+        a.prefill(b)  # destination not empty
+
+
+# ---------------------------------------------------------------------------
+# Window sizes (nanochat/gpt.py:285-312) against closed forms
+# ---------------------------------------------------------------------------
+def test_window_sizes_closed_form():
+    # short window = ceil(seq / 4 / 128) * 128; the last layer is always long
+    w = orc.compute_window_sizes(2048, "SSSL", 24)
+    assert [x[0] for x in w] == ([512, 512, 512, 2048] * 6)
+    w = orc.compute_window_sizes(4096, "SSSL", 26)
+    assert sum(1 for x in w if x[0] == 1024) == 19 and sum(1 for x in w if x[0] == 4096) == 7
+    assert w[-1] == (4096, 0) and w[-2] == (1024, 0)
+    assert orc.compute_window_sizes(1024, "L", 12) == [(1024, 0)] * 12
+    assert orc.compute_window_sizes(1000, "S", 3) == [(256, 0), (256, 0), (1000, 0)]
+    assert orc.compute_window_sizes(2048, "SL", 4) == [(512, 0), (2048, 0), (512, 0), (2048, 0)]
+
+
+def test_decode_bytes_closed_form():
+    # 20 layers x sum_b 5120 (s_b + 3) for d20 shapes (10/10 heads x 128, bf16)
+    s = [512, 1000, 2047]
+    assert orc.decode_bytes(s, 20, 10, 10, 128, 2) == 20 * sum(5120 * (x + 3) for x in s)
+    # a window caps the keys at w + 1
+    assert orc.decode_bytes([100], 1, 1, 1, 128, 2, windows=[9]) == 512 * 10 + 512 + 512
+    assert math.isclose(orc.softmax_scale(128), 128 ** -0.5)
