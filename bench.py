@@ -71,6 +71,24 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
+def copy_ceiling(dev, stream, nbytes=1 << 31, reps=10) -> float:
+    """Achievable streaming bandwidth on this GPU: torch's device copy of 2 GiB, read + write bytes."""
+    with torch.cuda.stream(stream):
+        src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            dst.copy_(src)
+        e1.record(stream)
+        stream.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """Time the oracle (reference fallback restated, row by row) on the host cores."""
     sys.path.insert(0, str(ROOT))
@@ -216,6 +234,8 @@ def main() -> int:
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"[bench] CPU baseline: {cpu}")
 
+    copy_gbps = copy_ceiling(dev, stream)
+    log(f"[bench] torch copy_ of 2 GiB: {copy_gbps:.0f} GB/s (read + write)")
     traffic = read_traffic()
     out = {
         "metric": METRIC,
@@ -237,6 +257,8 @@ def main() -> int:
             "cache_len": T_MAX, "timing": "HIP graph of all steps, HIP events on the launch stream",
         },
         "pct_of_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
+        "hbm_copy_gbps": round(copy_gbps, 1),
+        "pct_of_copy": round(100.0 * gbps / copy_gbps, 2),
         "tokens_per_s": round(BATCH * K / t_s, 1),
         "wall_ms_per_step": round(wall_s * 1e3 / K, 5),
         "eager_ms_per_step": round(eager_ms, 5) if eager_ms is not None else None,

@@ -112,10 +112,10 @@ int nc_kv_fanout(const nc_fanout_args* args, void* stream);
  * mask.  Output is (B, T_new, H, D), contiguous, in q's dtype; accumulation
  * is fp32.  The fused path (t_new == 1) appends and attends in one launch;
  * t_new > 1 appends first and then attends (two launches, same stream).
- * The workspace holds split-K partials and per-(row, head) counters: it must
- * be zero-filled before its first use and is left zeroed by every call, so a
- * caller keeps one workspace per stream.  Calls sharing a workspace must not
- * overlap in time (different streams need different workspaces).
+ * When a row's keys span several splits, partial results go to the workspace
+ * (nc_attn_workspace_bytes; 0 bytes when every row fits one split) and a
+ * second small kernel merges them.  The workspace needs no initialisation;
+ * calls sharing a workspace must not overlap in time (use one per stream).
  * ------------------------------------------------------------------------- */
 typedef struct nc_attn_args {
   const void* q;                 /* (B, T_new, H, D) */

@@ -7,12 +7,15 @@ missing, every call raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "libnc_kv.so"
+# NANOCHAT_AMD_LIB points at another build of the same library (e.g. a tuning
+# variant); by default the in-tree build next to this file is loaded.
+LIB_PATH = Path(os.environ.get("NANOCHAT_AMD_LIB", Path(__file__).resolve().parent / "libnc_kv.so"))
 ABI_VERSION = 1
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
@@ -119,9 +122,8 @@ def stream_handle(device: torch.device) -> int:
 
 
 # ---------------------------------------------------------------------------
-# Per-(device, stream) split-K workspace and per-device error flag.
-# The kernels leave the workspace's ticket counters at zero, so one zeroed
-# buffer per stream is reused across calls; calls on one stream are ordered.
+# Per-(device, stream) split-K workspace and per-device error flag.  Calls on
+# one stream are ordered, so one buffer per stream is reused across calls.
 # ---------------------------------------------------------------------------
 _workspaces: dict = {}
 _error_flags: dict = {}
@@ -134,7 +136,7 @@ def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | 
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
         cap = max(nbytes, 2 * buf.numel() if buf is not None else 0, 1 << 20)
-        buf = torch.zeros(cap, dtype=torch.uint8, device=device)
+        buf = torch.empty(cap, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf
 

@@ -43,30 +43,37 @@ def _hipcc() -> str:
     return path
 
 
-def _compile(src: str) -> Path:
-    obj = OBJ_DIR / (Path(src).stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)]
+def _compile(src: str, obj_dir: Path, extra: tuple) -> Path:
+    obj = obj_dir / (Path(src).stem + ".o")
+    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile all kernels for gfx950 and link nanochat_amd/libnc_kv.so."""
-    OBJ_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = True, defines: dict | None = None, out: Path | None = None) -> Path:
+    """Compile all kernels for gfx950 and link nanochat_amd/libnc_kv.so.
+
+    `defines` (e.g. {"NC_DECODE_WAVES": 8}) and `out` build a tuning variant
+    of the library at another path, leaving the in-tree build alone.
+    """
+    out = Path(out) if out is not None else LIB_PATH
+    extra = tuple(f"-D{k}={v}" for k, v in sorted((defines or {}).items()))
+    obj_dir = OBJ_DIR if not extra else OBJ_DIR / ("v_" + "_".join(f"{k}{v}" for k, v in sorted(defines.items())))
+    obj_dir.mkdir(parents=True, exist_ok=True)
     workers = min(len(SOURCES), max(1, (os.cpu_count() or 2) // 2), 8)
     with ThreadPoolExecutor(max_workers=workers) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda s: _compile(s, obj_dir, extra), SOURCES))
+    tmp = out.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB_PATH}", flush=True)
-    return LIB_PATH
+        print(f"built {out}", flush=True)
+    return out
 
 
 if __name__ == "__main__":

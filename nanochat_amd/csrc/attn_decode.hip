@@ -1,11 +1,11 @@
 // Split-K flash-decoding over the KV cache (nanochat/flash_attention.py:82-89,
 // 155-177 with FA3's per-row cache_seqlens), GQA and sliding window.
 //
-// Work decomposition: one workgroup per (row b, query t, kv head, q-head block,
-// key split).  A split is a contiguous run of `keys_per_split` cache positions
-// of one kv head; the workgroup streams it once from HBM and scores it against
-// every q head of its head block (GQA packing: the K/V bytes are read once for
-// all G = H / H_kv query heads).
+// Work decomposition.  A "unit" is one (kv head, q-head block): the GB query
+// heads of a kv head scored together (GQA packing: K/V bytes are read once for
+// all of them).  A workgroup is (row b, query t, unit, key split): 4 waves
+// that stream `keys_per_split` cache positions of the unit's kv head, tiles
+// interleaved across the waves.
 //
 // Lane layout inside a wave (D = head_dim, VEC = elements per 16 bytes):
 //   LPK = D / VEC lanes hold one key row (16 bytes each), KPI = 64 / LPK keys
@@ -13,27 +13,58 @@
 //   dot product finished by a DPP all-reduce over the LPK lanes, so every lane
 //   of a key group ends up with that key's score and no LDS traffic is needed
 //   in the streaming loop.  Each key group (`row`) keeps its own online-softmax
-//   state (max m, sum l, output o) and rows / waves are merged once at the end.
+//   state (max m, sum l, output o); rows are merged by a butterfly and waves
+//   through LDS once at the end.
 //
-// Split merge: a split writes (o, m, l) partials to the workspace; the last
-// workgroup of a (b, t, kv head, head block) to finish (atomic ticket) merges
-// them with the log-sum-exp rule and writes the output, then re-zeroes its
-// ticket.  Single-split rows write the output directly.
+// Split merge: rows whose keys fit one split write the output directly.  Longer
+// rows write (o, m, l) partials to the workspace and merge_splits_kernel, the
+// next launch on the stream, combines them with the log-sum-exp rule.  The
+// kernel boundary is the only synchronisation: an in-kernel "last split
+// merges" scheme needs agent-scope release fences (L2 write-back), which
+// measured 3-10x slower on MI355X.  The splits of one (b, t, unit) run on the
+// XCD of its merge block (workgroups are dispatched round-robin over the 8
+// XCDs), so the merge reads the partials from the L2 they were written to.
 //
 // Fused append (t_new == 1 with k/v given): the split owning position s_b
 // takes the new key/value from the k/v inputs (converted to the cache dtype,
-// RNE) instead of the cache, and head block 0 stores them into the cache.  No
-// other workgroup reads position s_b, so the store does not race.
+// RNE) instead of the cache, and the hb == 0 unit of each kv head stores them
+// into the cache.  No other workgroup reads position s_b, so the store does
+// not race.
+
+#include <algorithm>
 
 #include "nc_kv_common.hpp"
 #include "nc_kv_internal.hpp"
+
+// Compile-time tuning (defaults are the measured best on MI355X; see the
+// per-option notes).
+#ifndef NC_DECODE_WAVES
+#define NC_DECODE_WAVES 4       // waves per workgroup (8: -1%, 2: -6%)
+#endif
+#ifndef NC_DECODE_NI
+#define NC_DECODE_NI 8          // 16-byte K (and V) loads per lane per tile, GB < 4
+#endif
+#ifndef NC_DECODE_NI_GQA
+#define NC_DECODE_NI_GQA 4      // same for head blocks of 4 or 8 q heads
+#endif
+#ifndef NC_DECODE_XCD_MAP
+#define NC_DECODE_XCD_MAP 1     // 1: the splits of a unit run on the XCD of its merge block
+#endif
+#ifndef NC_DECODE_NT_LOADS
+#define NC_DECODE_NT_LOADS 1    // 1: K/V loads carry the non-temporal hint (+12% measured)
+#endif
+#ifndef NC_DECODE_KEY_BYTES
+#define NC_DECODE_KEY_BYTES 65536  // default split: this many K bytes per unit (and as many V)
+#endif
 
 namespace nckv {
 
 namespace {
 
-constexpr int kWavesPerWG = 4;
-constexpr float kNegBig = -1.0e30f;  // finite "minus infinity" for running maxima
+constexpr int kWavesPerWG = NC_DECODE_WAVES;
+constexpr float kNegBig = -1.0e30f;   // finite "minus infinity" for running maxima
+constexpr int kMaxMergeSplits = 256;  // split cap of the launch plan
+constexpr int kXcds = 8;              // MI355X: workgroups go round-robin over 8 XCDs
 
 struct DecodeParams {
   const void* q;
@@ -44,7 +75,6 @@ struct DecodeParams {
   const void* v_new;
   const int32_t* seqlens;
   int32_t* err;
-  int32_t* counters;
   float* part_ml;
   float* part_o;
   int64_t q_sb, q_st, q_sh;
@@ -53,6 +83,8 @@ struct DecodeParams {
   int64_t k_sb, k_st, k_sh;
   int64_t v_sb, v_st, v_sh;
   int32_t t_new, t_max, n_heads, n_kv_heads, group, n_hblocks;
+  int32_t n_units;   // n_kv_heads * n_hblocks
+  int64_t n_groups;  // B * t_new * n_units
   int32_t window;
   float scale_log2;
   int32_t q_dtype;
@@ -100,12 +132,106 @@ template <typename TC> struct QFrag<TC, false> {
   }
 };
 
+__device__ __forceinline__ uint4 load16(const char* p) {
+#if NC_DECODE_NT_LOADS
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
+// Key range [lo, hi) of query t of row b and its split count.
+struct KeyRange {
+  int qpos, lo, hi, n, nsplit;
+};
+
+__device__ __forceinline__ KeyRange key_range(const DecodeParams& p, int64_t b, int t) {
+  KeyRange r;
+  r.qpos = p.seqlens[b] + t;  // absolute position of the query
+  r.hi = min(r.qpos + 1, p.t_max);
+  r.lo = p.window >= 0 ? max(0, r.qpos - p.window) : 0;
+  r.n = r.hi - r.lo;
+  r.nsplit = r.n > 0 ? (r.n + p.keys_per_split - 1) / p.keys_per_split : 1;
+  return r;
+}
+
+// Group index -> (b, t, kv head, head block).
+struct GroupIdx {
+  int64_t b;
+  int t, hk, hb;
+};
+
+__device__ __forceinline__ GroupIdx group_index(const DecodeParams& p, int64_t group) {
+  GroupIdx r;
+  r.hb = static_cast<int>(group % p.n_hblocks);
+  group /= p.n_hblocks;
+  r.hk = static_cast<int>(group % p.n_kv_heads);
+  group /= p.n_kv_heads;
+  r.t = static_cast<int>(group % p.t_new);
+  r.b = group / p.t_new;
+  return r;
+}
+
+constexpr int kMergeChunk = 16;
+
+// Second pass: block g combines the split partials of group g's GB heads (rows
+// that used a single split were finished by the decode kernel).  Each thread
+// owns one output element and folds the splits in chunks of 16 with all loads
+// of a chunk in flight together, so up to 16 splits cost one memory round
+// trip; the (m, l) reads are uniform per head (one transaction per wave).
+template <int D, int GB>
+__global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p) {
+  const GroupIdx gi = group_index(p, blockIdx.x);
+  const int nsplit = key_range(p, gi.b, gi.t).nsplit;
+  if (nsplit <= 1) return;
+  const int64_t pair0 = (gi.b * p.t_new + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;
+  for (int idx = threadIdx.x; idx < GB * D; idx += blockDim.x) {
+    const int g = idx / D, d = idx % D;
+    const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
+    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d;
+    float M = kNegBig, L = 0.0f, O = 0.0f;
+    for (int sp0 = 0; sp0 < nsplit; sp0 += kMergeChunk) {
+      float ms[kMergeChunk], ls[kMergeChunk], os[kMergeChunk];
+#pragma unroll
+      for (int u = 0; u < kMergeChunk; ++u) {
+        const int sp = sp0 + u;
+        if (sp < nsplit) {
+          const float2 v = *reinterpret_cast<const float2*>(ml + 2 * sp);
+          ms[u] = v.x;
+          ls[u] = v.y;
+          os[u] = po[static_cast<int64_t>(sp) * D];
+        } else {
+          ms[u] = kNegBig;
+          ls[u] = 0.0f;
+          os[u] = 0.0f;
+        }
+      }
+      float mx = M;
+#pragma unroll
+      for (int u = 0; u < kMergeChunk; ++u) mx = fmaxf(mx, ms[u]);
+      const float a = fast_exp2(M - mx);
+      L *= a;
+      O *= a;
+#pragma unroll
+      for (int u = 0; u < kMergeChunk; ++u) {
+        const float w = fast_exp2(ms[u] - mx);
+        L = __builtin_fmaf(ls[u], w, L);
+        O = __builtin_fmaf(os[u], w, O);
+      }
+      M = mx;
+    }
+    store_any(p.out, (pair0 + g) * D + d, p.q_dtype, L > 0.0f ? O / L : 0.0f);
+  }
+}
+
 template <typename TC, bool QPK, int D, int GB>
 __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const DecodeParams p) {
   constexpr int VEC = widen<TC>::N;
   constexpr int LPK = D / VEC;            // lanes per key row
   constexpr int KPI = kWave / LPK;        // keys per load instruction
-  constexpr int NI = (GB >= 4) ? 4 : 8;   // load instructions per tile (K and V each)
+  constexpr int NI = (GB >= 4) ? NC_DECODE_NI_GQA : NC_DECODE_NI;  // loads per tile (K and V each)
   constexpr int TILE = KPI * NI;          // keys per wave tile
   constexpr int NW = kWavesPerWG;
   constexpr int EB = elem<TC>::kBytes;
@@ -116,7 +242,6 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
   __shared__ float sm_l[NW][GB];
   __shared__ float sm_w[NW][GB];
   __shared__ float sm_L[GB];
-  __shared__ int sm_last;
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -124,33 +249,36 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
   const int row = lane / LPK;
   const int col = lane % LPK;
 
-  // ---- block -> (b, t, kv head, head block, split) ----
-  int64_t wg = blockIdx.x;
-  const int split = static_cast<int>(wg % p.num_splits); wg /= p.num_splits;
-  const int hb = static_cast<int>(wg % p.n_hblocks); wg /= p.n_hblocks;
-  const int hk = static_cast<int>(wg % p.n_kv_heads); wg /= p.n_kv_heads;
-  const int t = static_cast<int>(wg % p.t_new);
-  const int64_t b = wg / p.t_new;
+  // ---- block -> (group, split) ----
+#if NC_DECODE_XCD_MAP
+  const int64_t pb = blockIdx.x;
+  const int64_t pr = pb / kXcds;
+  const int split = static_cast<int>(pr % p.num_splits);
+  const int64_t group = (pr / p.num_splits) * kXcds + pb % kXcds;
+  if (group >= p.n_groups) return;
+#else
+  const int split = static_cast<int>(blockIdx.x % p.num_splits);
+  const int64_t group = blockIdx.x / p.num_splits;
+#endif
+  const GroupIdx gi = group_index(p, group);
+  const int64_t b = gi.b;
+  const int t = gi.t, hk = gi.hk, hb = gi.hb;
 
-  const int s = p.seqlens[b];
-  const int qpos = s + t;                         // absolute position of the query
-  const int hi = min(qpos + 1, p.t_max);          // keys [lo, hi)
-  const int lo = p.window >= 0 ? max(0, qpos - p.window) : 0;
-  const int n = hi - lo;
-  const int nsplit = n > 0 ? (n + p.keys_per_split - 1) / p.keys_per_split : 1;
-  if (split >= nsplit) return;
-
-  const int k0 = lo + split * p.keys_per_split;
-  const int k1 = n > 0 ? min(k0 + p.keys_per_split, hi) : k0;
+  const KeyRange kr = key_range(p, b, t);
+  if (split >= kr.nsplit) return;
+  const int qpos = kr.qpos;
+  const int k0 = kr.lo + split * p.keys_per_split;
+  const int k1 = kr.n > 0 ? min(k0 + p.keys_per_split, kr.hi) : k0;
   const bool new_in_range = p.fused && qpos >= 0 && qpos < p.t_max;
-  const bool own_new = new_in_range && n > 0 && k1 == qpos + 1;
+  const bool own_new = new_in_range && kr.n > 0 && k1 == qpos + 1;
   const int kc_end = own_new ? k1 - 1 : k1;       // keys read from the cache: [k0, kc_end)
 
-  if (p.fused && (qpos < 0 || qpos >= p.t_max) && split == 0 && hb == 0 && tid == 0 && p.err != nullptr) {
+  if (p.fused && (qpos < 0 || qpos >= p.t_max) && split == 0 && hk == 0 && hb == 0 && tid == 0 &&
+      p.err != nullptr) {
     atomicOr(p.err, NC_DEVERR_OVERFLOW);
   }
 
-  const int h0 = hk * p.group + hb * GB;          // first q head of this block
+  const int h0 = hk * p.group + hb * GB;          // first q head of this unit
 
   // ---- query fragments ----
   QFrag<TC, QPK> qf[GB];
@@ -186,8 +314,8 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
     for (int i = 0; i < NI; ++i) {
       const int j = base + i * KPI + row;
       if (j < kc_end) {
-        kv[i] = *reinterpret_cast<const uint4*>(kbase + j * kst);
-        vv[i] = *reinterpret_cast<const uint4*>(vbase + j * vst);
+        kv[i] = load16(kbase + j * kst);
+        vv[i] = load16(vbase + j * vst);
       } else {
         kv[i] = make_uint4(0, 0, 0, 0);
         vv[i] = make_uint4(0, 0, 0, 0);
@@ -301,12 +429,12 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
       L += sm_l[w][g] * wt;
     }
     sm_L[g] = L;
-    sm_m[0][g] = mx;  // keep the merged max in slot 0 (read below)
+    sm_m[0][g] = mx;  // merged max, read below
   }
   __syncthreads();
 
   const int64_t pair0 = (b * p.t_new + t) * p.n_heads + h0;  // (b, t, h0)
-  if (nsplit == 1) {
+  if (kr.nsplit == 1) {
     for (int idx = tid; idx < GB * D; idx += NW * kWave) {
       const int g = idx / D, d = idx % D;
       float acc = 0.0f;
@@ -317,7 +445,6 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
     }
     return;
   }
-
   for (int idx = tid; idx < GB * D; idx += NW * kWave) {
     const int g = idx / D, d = idx % D;
     float acc = 0.0f;
@@ -326,66 +453,31 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
     p.part_o[((pair0 + g) * p.num_splits + split) * D + d] = acc;
   }
   if (tid < GB) {
-    float* ml = p.part_ml + ((pair0 + tid) * p.num_splits + split) * 2;
-    ml[0] = sm_m[0][tid];
-    ml[1] = sm_L[tid];
+    *reinterpret_cast<float2*>(p.part_ml + ((pair0 + tid) * p.num_splits + split) * 2) =
+        make_float2(sm_m[0][tid], sm_L[tid]);
   }
+}
 
-  // ---- last split of this (b, t, kv head, head block) merges all partials ----
-  __threadfence();
-  __syncthreads();
-  const int64_t ctr = ((b * p.t_new + t) * p.n_kv_heads + hk) * p.n_hblocks + hb;
-  if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(p.counters + ctr, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    sm_last = (prev == nsplit - 1) ? 1 : 0;
+template <typename TC, bool QPK, int D, int GB>
+hipError_t launch_g(const DecodeParams& p, int64_t n_wg, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB>), dim3(static_cast<unsigned>(n_wg)),
+                     dim3(kWavesPerWG * kWave), 0, stream, p);
+  if (p.num_splits > 1) {
+    const int threads = std::min(256, (GB * D + kWave - 1) / kWave * kWave);
+    hipLaunchKernelGGL((merge_splits_kernel<D, GB>), dim3(static_cast<unsigned>(p.n_groups)), dim3(threads), 0,
+                       stream, p);
   }
-  __syncthreads();
-  if (!sm_last) return;
-  __threadfence();
-
-  // sm_o[0] is reused to hold per-split weights: (g, split) for split < nsplit.
-  float* wts = &sm_o[0][0][0];
-  const int wcap = NW * GB * D / GB;  // weights slots per head
-  if (tid < GB) {
-    const int g = tid;
-    const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
-    float mx = kNegBig;
-    for (int sp = 0; sp < nsplit; ++sp) {
-      mx = fmaxf(mx, __hip_atomic_load(ml + 2 * sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    }
-    float L = 0.0f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const float ms = __hip_atomic_load(ml + 2 * sp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float ls = __hip_atomic_load(ml + 2 * sp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float wt = fast_exp2(ms - mx);
-      if (sp < wcap) wts[g * wcap + sp] = wt;
-      L += ls * wt;
-    }
-    sm_L[g] = L;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < GB * D; idx += NW * kWave) {
-    const int g = idx / D, d = idx % D;
-    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d;
-    float acc = 0.0f;
-    for (int sp = 0; sp < nsplit; ++sp) acc += po[static_cast<int64_t>(sp) * D] * wts[g * wcap + sp];
-    const float L = sm_L[g];
-    store_any(p.out, (pair0 + g) * D + d, p.q_dtype, L > 0.0f ? acc / L : 0.0f);
-  }
-  if (tid == 0) __hip_atomic_store(p.counters + ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return hipGetLastError();
 }
 
 template <typename TC, bool QPK, int D>
 hipError_t launch_d(const DecodeParams& p, int gb, int64_t n_wg, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(n_wg));
-  const dim3 block(kWavesPerWG * kWave);
   switch (gb) {
-    case 8: hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, 8>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, 4>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, 2>), grid, block, 0, stream, p); break;
-    default: hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, 1>), grid, block, 0, stream, p); break;
+    case 8: return launch_g<TC, QPK, D, 8>(p, n_wg, stream);
+    case 4: return launch_g<TC, QPK, D, 4>(p, n_wg, stream);
+    case 2: return launch_g<TC, QPK, D, 2>(p, n_wg, stream);
+    default: return launch_g<TC, QPK, D, 1>(p, n_wg, stream);
   }
-  return hipGetLastError();
 }
 
 template <typename TC, bool QPK>
@@ -405,7 +497,17 @@ bool decode_supports(int cache_dtype, int64_t head_dim) {
   return head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256;
 }
 
-int split_weight_capacity(int64_t head_dim) { return kWavesPerWG * static_cast<int>(head_dim); }
+int max_splits() { return kMaxMergeSplits; }
+
+int default_split_bytes() { return NC_DECODE_KEY_BYTES; }
+
+int64_t decode_grid(int64_t n_groups, int num_splits) {
+#if NC_DECODE_XCD_MAP
+  return kXcds * num_splits * ((n_groups + kXcds - 1) / kXcds);
+#else
+  return num_splits * n_groups;
+#endif
+}
 
 hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
                          bool fused_append, hipStream_t stream) {
@@ -414,7 +516,7 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.kc = static_cast<char*>(a.k_cache); p.vc = static_cast<char*>(a.v_cache);
   p.k_new = a.k; p.v_new = a.v;
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
-  p.counters = s.counters; p.part_ml = s.part_ml; p.part_o = s.part_o;
+  p.part_ml = s.part_ml; p.part_o = s.part_o;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
@@ -426,6 +528,8 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.n_kv_heads = static_cast<int32_t>(a.n_kv_heads);
   p.group = plan.group;
   p.n_hblocks = plan.n_hblocks;
+  p.n_units = plan.n_units;
+  p.n_groups = plan.n_groups;
   p.window = a.window_left;
   p.scale_log2 = a.softmax_scale * 1.4426950408889634f;
   p.q_dtype = a.q_dtype;
@@ -433,15 +537,16 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.keys_per_split = plan.keys_per_split;
   p.fused = fused_append ? 1 : 0;
   const bool qpk = a.q_dtype == a.cache_dtype && a.cache_dtype != NC_DTYPE_F32;
+  const int gb = plan.head_block;
   switch (a.cache_dtype) {
     case NC_DTYPE_BF16:
-      return qpk ? launch_dt<bf16, true>(p, a.head_dim, plan.head_block, plan.n_wg, stream)
-                 : launch_dt<bf16, false>(p, a.head_dim, plan.head_block, plan.n_wg, stream);
+      return qpk ? launch_dt<bf16, true>(p, a.head_dim, gb, plan.n_wg, stream)
+                 : launch_dt<bf16, false>(p, a.head_dim, gb, plan.n_wg, stream);
     case NC_DTYPE_F16:
-      return qpk ? launch_dt<f16, true>(p, a.head_dim, plan.head_block, plan.n_wg, stream)
-                 : launch_dt<f16, false>(p, a.head_dim, plan.head_block, plan.n_wg, stream);
+      return qpk ? launch_dt<f16, true>(p, a.head_dim, gb, plan.n_wg, stream)
+                 : launch_dt<f16, false>(p, a.head_dim, gb, plan.n_wg, stream);
     default:
-      return launch_dt<float, false>(p, a.head_dim, plan.head_block, plan.n_wg, stream);
+      return launch_dt<float, false>(p, a.head_dim, gb, plan.n_wg, stream);
   }
 }
 

@@ -10,11 +10,7 @@
 
 namespace nckv {
 
-int split_weight_capacity(int64_t head_dim);
-
 namespace {
-
-constexpr int kMaxSplits = 256;
 
 bool valid_dtype(int d) { return d == NC_DTYPE_F32 || d == NC_DTYPE_F16 || d == NC_DTYPE_BF16; }
 int64_t dtype_bytes(int d) { return d == NC_DTYPE_F32 ? 4 : 2; }
@@ -45,15 +41,17 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   plan->group = group;
   plan->head_block = hb;
   plan->n_hblocks = group / hb;
+  if (a.n_kv_heads * plan->n_hblocks > INT32_MAX / 2) return NC_ERR_BAD_SHAPE;
+  plan->n_units = static_cast<int>(a.n_kv_heads) * plan->n_hblocks;
+  plan->n_groups = a.batch * a.t_new * plan->n_units;
 
   const int64_t ebytes = dtype_bytes(a.cache_dtype);
   const int64_t max_keys = a.window_left >= 0 ? std::min<int64_t>(a.t_max, int64_t(a.window_left) + 1) : a.t_max;
   int64_t kps = a.keys_per_split;
   if (kps == 0) {
-    // ~64 KiB of K (and as much V) per workgroup.
-    kps = std::max<int64_t>(64, (65536 / (a.head_dim * ebytes)) / 64 * 64);
+    kps = std::max<int64_t>(64, (default_split_bytes() / (a.head_dim * ebytes) + 63) / 64 * 64);
   }
-  const int64_t cap = std::min<int64_t>(kMaxSplits, split_weight_capacity(a.head_dim));
+  const int64_t cap = max_splits();
   int64_t ns = (max_keys + kps - 1) / kps;
   if (ns > cap) {
     kps = ((max_keys + cap - 1) / cap + 63) / 64 * 64;
@@ -61,18 +59,17 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   }
   plan->keys_per_split = static_cast<int>(kps);
   plan->num_splits = static_cast<int>(ns);
-  plan->n_wg = a.batch * a.t_new * a.n_kv_heads * plan->n_hblocks * ns;
-  if (plan->n_wg <= 0 || plan->n_wg > INT32_MAX) return NC_ERR_BAD_SHAPE;
+  plan->n_wg = decode_grid(plan->n_groups, plan->num_splits);
+  if (plan->n_groups <= 0 || plan->n_wg <= 0 || plan->n_wg > INT32_MAX) return NC_ERR_BAD_SHAPE;
 
   if (ns > 1) {
     const size_t pairs = static_cast<size_t>(a.batch * a.t_new * a.n_heads);
-    plan->counters_bytes = round256(static_cast<size_t>(a.batch * a.t_new * a.n_kv_heads * plan->n_hblocks) * 4);
     plan->ml_bytes = round256(pairs * ns * 2 * 4);
     plan->o_bytes = round256(pairs * ns * static_cast<size_t>(a.head_dim) * 4);
   } else {
-    plan->counters_bytes = plan->ml_bytes = plan->o_bytes = 0;
+    plan->ml_bytes = plan->o_bytes = 0;
   }
-  plan->total_bytes = plan->counters_bytes + plan->ml_bytes + plan->o_bytes;
+  plan->total_bytes = plan->ml_bytes + plan->o_bytes;
   return NC_OK;
 }
 
@@ -182,9 +179,8 @@ int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
 
   AttnScratch s;
   char* ws = static_cast<char*>(a.workspace);
-  s.counters = reinterpret_cast<int32_t*>(ws);
-  s.part_ml = reinterpret_cast<float*>(ws + plan.counters_bytes);
-  s.part_o = reinterpret_cast<float*>(ws + plan.counters_bytes + plan.ml_bytes);
+  s.part_ml = reinterpret_cast<float*>(ws);
+  s.part_o = reinterpret_cast<float*>(ws + plan.ml_bytes);
   hipStream_t hs = static_cast<hipStream_t>(stream);
 
   bool fused = false;

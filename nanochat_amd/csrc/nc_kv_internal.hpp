@@ -11,7 +11,6 @@ namespace nckv {
 
 // Split-K scratch carved out of the caller's workspace.
 struct AttnScratch {
-  int32_t* counters;   // one per (row, query, kv head, head block); zero between calls
   float* part_ml;      // (pair, split, 2): running max (log2 domain) and sum
   float* part_o;       // (pair, split, D): unnormalised output
 };
@@ -19,12 +18,14 @@ struct AttnScratch {
 // Launch plan shared by nc_attn_workspace_bytes and nc_attn_kvcache.
 struct AttnPlan {
   int group;           // q heads per kv head
-  int head_block;      // q heads one workgroup handles (divides group)
+  int head_block;      // q heads one workgroup scores together (divides group)
   int n_hblocks;       // group / head_block
+  int n_units;         // n_kv_heads * n_hblocks
+  int64_t n_groups;    // batch * t_new * n_units: one merge block each
   int keys_per_split;
   int num_splits;
-  int64_t n_wg;
-  size_t counters_bytes, ml_bytes, o_bytes, total_bytes;
+  int64_t n_wg;        // decode grid size
+  size_t ml_bytes, o_bytes, total_bytes;
 };
 
 // Returns NC_OK and fills `plan`, or an error code.
@@ -36,5 +37,8 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
                          bool fused_append, hipStream_t stream);
 
 bool decode_supports(int cache_dtype, int64_t head_dim);
+int max_splits();
+int default_split_bytes();
+int64_t decode_grid(int64_t n_groups, int num_splits);
 
 }  // namespace nckv

@@ -71,17 +71,21 @@ def _attn_args(B=32, T_new=1, T_max=2304, H=10, H_kv=10, D=128, window=-1, dtype
 def test_workspace_plan_for_d20_decode():
     lib = _ext.lib()
     a = _attn_args()
-    # 2304 keys / 256 keys per split = 9 splits; counters + (m, l) + o partials
+    # 64 KiB of K per head per split -> 256 keys; 2304 / 256 = 9 splits;
+    # (m, l) and o partials per (row, head, split)
     pairs = 32 * 10
-    expect = 256 * ((32 * 10 * 4 + 255) // 256) + 256 * ((pairs * 9 * 8 + 255) // 256) + pairs * 9 * 128 * 4
+    expect = 256 * ((pairs * 9 * 8 + 255) // 256) + pairs * 9 * 128 * 4
     assert lib.nc_attn_workspace_bytes(ctypes.byref(a)) == expect
 
 
 def test_workspace_zero_for_single_split_and_window_caps_keys():
     lib = _ext.lib()
-    assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=200))) == 0
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=256))) == 0
     assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=4096, window=255))) == 0
     assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=4096, window=256))) > 0
+    # split cap: 65536 keys at the 256-key default is exactly 256 splits; 80000 keys widen the split
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(B=1, H=1, H_kv=1, T_max=80000))) == \
+        256 * ((1 * 250 * 8 + 255) // 256) + 250 * 128 * 4
 
 
 def test_invalid_arguments_are_rejected_before_launch():

@@ -118,9 +118,18 @@ def test_decode_dtypes(q_dtype, cache_dtype):
     _check(40, 3, 1, 8, 4, 128, 400, [17, 256, 399], 100, q_dtype=q_dtype, cache_dtype=cache_dtype, kps=128)
 
 
-@pytest.mark.parametrize("kps", [0, 64, 128, 512])
+@pytest.mark.parametrize("kps", [0, 64, 128, 512, 1152])
 def test_decode_split_sizes_agree(kps):
     _check(50, 6, 1, 10, 10, 128, 1100, [0, 1, 511, 512, 513, 1099], -1, kps=kps)
+
+
+def test_chunk_split_merge():
+    _check(51, 2, 5, 8, 2, 128, 900, [0, 700], -1, kps=64)
+
+
+def test_decode_many_splits_cap():
+    """16384 keys at 64 keys per split exceed the 256-split cap: the plan widens the splits."""
+    _check(52, 2, 1, 4, 1, 64, 16384, [16383, 9000], -1, kps=64)
 
 
 def test_decode_without_new_kv_reads_cache_only():
@@ -128,7 +137,7 @@ def test_decode_without_new_kv_reads_cache_only():
 
 
 def test_decode_repeated_calls_reuse_workspace():
-    """The split tickets reset themselves: many calls in a row stay correct."""
+    """The per-stream workspace is reused: many calls in a row stay correct."""
     for i in range(5):
         _check(70 + i, 4, 1, 8, 8, 128, 600, [100 * (i + 1), 7, 599 - i, 300], -1, kps=64)
 
