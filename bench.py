@@ -63,12 +63,18 @@ def step_bytes(seqlens, layers=LAYERS) -> int:
 
 
 def read_traffic():
-    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, or None."""
+    """(HBM bytes, algorithmic bytes) per call from the committed rocprofv3 --pmc summary, or None.
+
+    The PMC runs (profiles/attn_decode_d20_pmc.md) measure FETCH_SIZE and WRITE_SIZE per
+    dispatch, scaled by the same counters' reading for a 2 GiB copy kernel.
+    """
     path = ROOT / "profiles" / "attn_decode_d20_pmc.md"
     if not path.exists():
         return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)\s*$", path.read_text(), flags=re.M)
-    return float(m.group(1)) if m else None
+    text = path.read_text()
+    t = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)\s*$", text, flags=re.M)
+    a = re.search(r"^algorithmic_bytes_per_launch:\s*([0-9.eE+]+)\s*$", text, flags=re.M)
+    return (float(t.group(1)), float(a.group(1))) if t and a else None
 
 
 def copy_ceiling(dev, stream, nbytes=1 << 31, reps=10) -> float:
@@ -268,8 +274,10 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(bytes_per_launch / (avg_launch_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-            "traffic": traffic,
-            "kernel": "decode_attn_kernel<bf16, packed-q, D=128, GB=1> (fused append + split-K + merge)",
+            "traffic": traffic[0] if traffic else None,
+            "traffic_over_algorithmic": round(traffic[0] / traffic[1], 4) if traffic else None,
+            "kernel": "one flash_attn_with_kvcache decode call: decode_attn_kernel<bf16, packed-q, D=128, GB=1> "
+                      "(fused append + split-K) + merge_splits_kernel<128, 1>",
             "avg_launch_us": round(avg_launch_us, 3),
             "algorithmic_bytes_per_launch": round(bytes_per_launch),
         },

@@ -16,9 +16,11 @@
 //   state (max m, sum l, output o); rows are merged by a butterfly and waves
 //   through LDS once at the end.
 //
-// Split merge: rows whose keys fit one split write the output directly.  Longer
-// rows write (o, m, l) partials to the workspace and merge_splits_kernel, the
-// next launch on the stream, combines them with the log-sum-exp rule.  The
+// Split merge: when the plan has one split the decode kernel writes the output.
+// Otherwise every split writes (o, m, l) partials to the workspace (a split
+// past the end of its row writes only l = 0, which marks it empty) and
+// merge_splits_kernel, the next launch on the stream, combines all split slots
+// with the log-sum-exp rule without re-reading cache_seqlens.  The
 // kernel boundary is the only synchronisation: an in-kernel "last split
 // merges" scheme needs agent-scope release fences (L2 write-back), which
 // measured 3-10x slower on MI355X.  The splits of one (b, t, unit) run on the
@@ -176,21 +178,21 @@ __device__ __forceinline__ GroupIdx group_index(const DecodeParams& p, int64_t g
 
 constexpr int kMergeChunk = 16;
 
-// Second pass: block g combines the split partials of group g's GB heads (rows
-// that used a single split were finished by the decode kernel).  Each thread
-// owns one output element and folds the splits in chunks of 16 with all loads
-// of a chunk in flight together, so up to 16 splits cost one memory round
-// trip; the (m, l) reads are uniform per head (one transaction per wave).
+// Second pass: block g combines the split partials of group g's GB heads.
+// Each thread owns one output element and folds the split slots in chunks of
+// 16 with all loads of a chunk in flight together, so up to 16 splits cost
+// one memory round trip; the (m, l) reads are uniform per head (one
+// transaction per wave).  Slots with l == 0 are empty and contribute nothing
+// (their o was never written).
 template <int D, int GB>
 __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p) {
   const GroupIdx gi = group_index(p, blockIdx.x);
-  const int nsplit = key_range(p, gi.b, gi.t).nsplit;
-  if (nsplit <= 1) return;
+  const int nsplit = p.num_splits;
   const int64_t pair0 = (gi.b * p.t_new + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;
   for (int idx = threadIdx.x; idx < GB * D; idx += blockDim.x) {
     const int g = idx / D, d = idx % D;
-    const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
-    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d;
+    const float* ml = p.part_ml + (pair0 + g) * nsplit * 2;
+    const float* po = p.part_o + (pair0 + g) * nsplit * D + d;
     float M = kNegBig, L = 0.0f, O = 0.0f;
     for (int sp0 = 0; sp0 < nsplit; sp0 += kMergeChunk) {
       float ms[kMergeChunk], ls[kMergeChunk], os[kMergeChunk];
@@ -210,15 +212,15 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
       }
       float mx = M;
 #pragma unroll
-      for (int u = 0; u < kMergeChunk; ++u) mx = fmaxf(mx, ms[u]);
+      for (int u = 0; u < kMergeChunk; ++u) mx = ls[u] > 0.0f ? fmaxf(mx, ms[u]) : mx;
       const float a = fast_exp2(M - mx);
       L *= a;
       O *= a;
 #pragma unroll
       for (int u = 0; u < kMergeChunk; ++u) {
-        const float w = fast_exp2(ms[u] - mx);
+        const float w = ls[u] > 0.0f ? fast_exp2(ms[u] - mx) : 0.0f;
         L = __builtin_fmaf(ls[u], w, L);
-        O = __builtin_fmaf(os[u], w, O);
+        O = ls[u] > 0.0f ? __builtin_fmaf(os[u], w, O) : O;
       }
       M = mx;
     }
@@ -265,7 +267,11 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
   const int t = gi.t, hk = gi.hk, hb = gi.hb;
 
   const KeyRange kr = key_range(p, b, t);
-  if (split >= kr.nsplit) return;
+  const int64_t pair0 = (b * p.t_new + t) * p.n_heads + hk * p.group + hb * GB;  // (b, t, first q head)
+  if (split >= kr.nsplit) {
+    if (tid < GB) p.part_ml[((pair0 + tid) * p.num_splits + split) * 2 + 1] = 0.0f;  // empty slot
+    return;
+  }
   const int qpos = kr.qpos;
   const int k0 = kr.lo + split * p.keys_per_split;
   const int k1 = kr.n > 0 ? min(k0 + p.keys_per_split, kr.hi) : k0;
@@ -433,8 +439,7 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
   }
   __syncthreads();
 
-  const int64_t pair0 = (b * p.t_new + t) * p.n_heads + h0;  // (b, t, h0)
-  if (kr.nsplit == 1) {
+  if (p.num_splits == 1) {
     for (int idx = tid; idx < GB * D; idx += NW * kWave) {
       const int g = idx / D, d = idx % D;
       float acc = 0.0f;
