@@ -6,12 +6,21 @@ methods reset / get_pos / get_layer_cache / advance / prefill).  The fan-out
 copy in ``prefill`` is one HIP launch (nc_kv_fanout) that reads the prefilled
 row once and writes it into every destination row, K and V of all layers,
 and sets cache_seqlens on the device.
+
+``Engine`` (generate / generate_batch), ``sample_next_token``, ``RowState``
+and ``use_calculator`` are the driver of nanochat/engine.py:25-304: one
+batch-1 prefill, fan-out to num_samples rows, then the decode loop with the
+per-row tool-use state machine.
 """
 from __future__ import annotations
 
+import ast
 import ctypes
+import operator
+from collections import deque
 
 import torch
+import torch.nn.functional as F
 
 from . import _ext
 
@@ -91,3 +100,169 @@ class KVCache:
         _ext.check(_ext.lib().nc_kv_fanout(ctypes.byref(a), _ext.stream_handle(dev)), "nc_kv_fanout")
         if other.prev_embedding is not None:
             self.prev_embedding = other.prev_embedding.expand(self.batch_size, -1, -1).clone()
+
+
+# ---------------------------------------------------------------------------
+# Engine: the driver of the path (nanochat/engine.py:140-304).  Same
+# allocation sizes, dtype rule, fan-out, per-row state machine and stop rules.
+# ---------------------------------------------------------------------------
+_ARITH = {ast.Add: operator.add, ast.Sub: operator.sub, ast.Mult: operator.mul, ast.Div: operator.truediv}
+_UNARY = {ast.UAdd: operator.pos, ast.USub: operator.neg}
+_MATH_CHARS = set("0123456789*+-/.() ")
+_STRING_CHARS = set("abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ0123456789'\"()._ ")
+_BANNED = ("__", "import", "exec", "eval", "compile", "open", "file", "input", "raw_input", "globals", "locals",
+           "vars", "dir", "getattr", "setattr", "delattr", "hasattr")
+
+
+def _eval_node(node):
+    if isinstance(node, ast.Expression):
+        return _eval_node(node.body)
+    if isinstance(node, ast.Constant) and type(node.value) in (int, float, str):
+        return node.value
+    if isinstance(node, ast.BinOp) and type(node.op) in _ARITH:
+        return _ARITH[type(node.op)](_eval_node(node.left), _eval_node(node.right))
+    if isinstance(node, ast.UnaryOp) and type(node.op) in _UNARY:
+        return _UNARY[type(node.op)](_eval_node(node.operand))
+    if (isinstance(node, ast.Call) and isinstance(node.func, ast.Attribute) and node.func.attr == "count"
+            and not node.keywords and len(node.args) == 1):
+        target, arg = _eval_node(node.func.value), _eval_node(node.args[0])
+        if isinstance(target, str) and isinstance(arg, str):
+            return target.count(arg)
+    raise ValueError("unsupported expression")
+
+
+def use_calculator(expr):
+    """The calculator tool of nanochat/engine.py:46-79: arithmetic (+ - * / and
+    parentheses, no power) or a string literal's .count(...); None when the
+    expression is not allowed or does not evaluate.  Evaluated by walking the
+    parsed expression over that closed set of node types (nothing is exec'd)."""
+    expr = expr.replace(",", "")
+    if all(c in _MATH_CHARS for c in expr):
+        if "**" in expr:
+            return None
+    else:
+        if not all(c in _STRING_CHARS for c in expr):
+            return None
+        lowered = expr.lower()
+        if any(p in lowered for p in _BANNED) or ".count(" not in expr:
+            return None
+    try:
+        return _eval_node(ast.parse(expr, mode="eval"))
+    except Exception:
+        return None
+
+
+@torch.inference_mode()
+def sample_next_token(logits, rng, temperature=1.0, top_k=None):
+    """(B, vocab) logits -> (B, 1) ids; nanochat/engine.py:140-156."""
+    assert temperature >= 0.0, "temperature must be non-negative"
+    if temperature == 0.0:
+        return torch.argmax(logits, dim=-1, keepdim=True)
+    if top_k is not None and top_k > 0:
+        k = min(top_k, logits.size(-1))
+        vals, idx = torch.topk(logits, k, dim=-1)
+        probs = F.softmax(vals / temperature, dim=-1)
+        choice = torch.multinomial(probs, num_samples=1, generator=rng)
+        return idx.gather(1, choice)
+    probs = F.softmax(logits / temperature, dim=-1)
+    return torch.multinomial(probs, num_samples=1, generator=rng)
+
+
+class RowState:
+    """Per-row generation state (tokens so far, forced tool tokens, python block)."""
+
+    def __init__(self, current_tokens=None):
+        self.current_tokens = current_tokens or []
+        self.forced_tokens = deque()
+        self.in_python_block = False
+        self.python_expr_tokens = []
+        self.completed = False
+
+
+class Engine:
+    """Batched generation with one prefill and a fanned-out KV cache."""
+
+    def __init__(self, model, tokenizer):
+        self.model = model
+        self.tokenizer = tokenizer
+
+    @torch.inference_mode()
+    def generate(self, tokens, num_samples=1, max_tokens=None, temperature=1.0, top_k=None, seed=42):
+        """Yield (token_column, token_masks) per step; nanochat/engine.py:176-280."""
+        assert isinstance(tokens, list) and isinstance(tokens[0], int), "expecting list of ints"
+        device = self.model.get_device()
+        dtype = torch.bfloat16 if device.type == "cuda" else torch.float32
+        rng = torch.Generator(device=device)
+        rng.manual_seed(seed)
+        special = self.tokenizer.encode_special
+        python_start, python_end = special("<|python_start|>"), special("<|python_end|>")
+        output_start, output_end = special("<|output_start|>"), special("<|output_end|>")
+        assistant_end = special("<|assistant_end|>")
+        bos = self.tokenizer.get_bos_token_id()
+
+        m = self.model.config
+        shape = dict(num_heads=m.n_kv_head, head_dim=m.n_embd // m.n_head, num_layers=m.n_layer)
+        prefill_cache = KVCache(batch_size=1, seq_len=len(tokens), device=device, dtype=dtype, **shape)
+        ids = torch.tensor([tokens], dtype=torch.long, device=device)
+        logits = self.model.forward(ids, kv_cache=prefill_cache)
+        logits = logits[:, -1, :].expand(num_samples, -1)
+
+        decode_len = (len(tokens) + max_tokens) if max_tokens is not None else self.model.config.sequence_len
+        cache = KVCache(batch_size=num_samples, seq_len=decode_len, device=device, dtype=dtype, **shape)
+        cache.prefill(prefill_cache)
+        del prefill_cache
+
+        rows = [RowState(tokens.copy()) for _ in range(num_samples)]
+        generated = 0
+        while True:
+            if max_tokens is not None and generated >= max_tokens:
+                break
+            if all(r.completed for r in rows):
+                break
+            sampled = sample_next_token(logits, rng, temperature, top_k)[:, 0].tolist()
+            column, masks = [], []
+            for i, r in enumerate(rows):
+                forced = len(r.forced_tokens) > 0
+                masks.append(0 if forced else 1)
+                tok = r.forced_tokens.popleft() if forced else sampled[i]
+                column.append(tok)
+                r.current_tokens.append(tok)
+                if tok == assistant_end or tok == bos:
+                    r.completed = True
+                if tok == python_start:
+                    r.in_python_block = True
+                    r.python_expr_tokens = []
+                elif tok == python_end and r.in_python_block:
+                    r.in_python_block = False
+                    if r.python_expr_tokens:
+                        result = use_calculator(self.tokenizer.decode(r.python_expr_tokens))
+                        if result is not None:
+                            r.forced_tokens.append(output_start)
+                            r.forced_tokens.extend(self.tokenizer.encode(str(result)))
+                            r.forced_tokens.append(output_end)
+                    r.python_expr_tokens = []
+                elif r.in_python_block:
+                    r.python_expr_tokens.append(tok)
+            yield column, masks
+            generated += 1
+            ids = torch.tensor(column, dtype=torch.long, device=device).unsqueeze(1)
+            logits = self.model.forward(ids, kv_cache=cache)[:, -1, :]
+
+    def generate_batch(self, tokens, num_samples=1, **kwargs):
+        """Final sequences (terminal tokens dropped) and masks; nanochat/engine.py:282-304."""
+        assistant_end = self.tokenizer.encode_special("<|assistant_end|>")
+        bos = self.tokenizer.get_bos_token_id()
+        results = [tokens.copy() for _ in range(num_samples)]
+        masks = [[0] * len(tokens) for _ in range(num_samples)]
+        completed = [False] * num_samples
+        for column, column_masks in self.generate(tokens, num_samples, **kwargs):
+            for i, (tok, mask) in enumerate(zip(column, column_masks)):
+                if not completed[i]:
+                    if tok == assistant_end or tok == bos:
+                        completed[i] = True
+                    else:
+                        results[i].append(tok)
+                        masks[i].append(mask)
+            if all(completed):
+                break
+        return results, masks

@@ -7,6 +7,7 @@ never imports it.
 
 It restates, with the same torch operations the reference uses:
   - _sdpa_attention            nanochat/flash_attention.py:69-102
+  - flash_attn_func            nanochat/flash_attention.py:107-128
   - flash_attn_with_kvcache    nanochat/flash_attention.py:155-177, applied row
                                by row with each row's own cache_seqlens[b] (FA3's
                                per-row contract, nanochat/engine.py:84-90); for a
@@ -52,6 +53,13 @@ def sdpa_attention(q, k, v, window_size, enable_gqa):
     if 0 <= window < Tk:
         mask = mask & ((row_idx - col_idx) <= window)
     return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=enable_gqa)
+
+
+def flash_attn_func(q, k, v, causal=False, window_size=(-1, -1)):
+    """nanochat/flash_attention.py:107-128 (the SDPA fallback): (B, T, H, D) in and out."""
+    q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    y = sdpa_attention(q, k, v, window_size, q.size(1) != k.size(1))
+    return y.transpose(1, 2)
 
 
 def kv_append(k_cache, v_cache, k, v, cache_seqlens):
