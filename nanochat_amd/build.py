@@ -23,7 +23,7 @@ LIB_PATH = PKG_DIR / LIB_NAME
 OBJ_DIR = PKG_DIR / "_build"
 ARCH = "gfx950"
 
-SOURCES = ["nc_kv_abi.hip", "kv_copy.hip", "attn_decode.hip"]
+SOURCES = ["nc_kv_abi.hip", "kv_copy.hip", "attn_decode.hip", "attn_chunk.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -1,0 +1,319 @@
+// Chunked prefill into the KV cache on MFMA (nanochat/flash_attention.py:91-102:
+// queries bottom-right aligned at s_b + i, causal, sliding window, GQA),
+// for T_new > 1 with bf16 / fp16 caches.  The new tokens are already in the
+// cache (kv_append_kernel runs first on the stream).
+//
+// Tiling.  A workgroup owns 64 "rows" = (query, q head) pairs of one
+// (row b, kv head, q-head block): 64 / GB queries x GB heads, so the GB heads
+// that share a kv head read each K/V tile once.  4 waves x 16 rows.  Key tiles
+// of 64 positions are staged in LDS: K as [key][dim] and V transposed as
+// [dim][key], both padded so the MFMA operand reads are bank-conflict free.
+//
+// Per tile and wave (v_mfma_f32_16x16x32_{bf16,f16}; lane l, q = l / 16):
+//   S^T = K . Q^T   A = K[16 keys][32 dims] (LDS), B = Q^T (registers);
+//                   lane l holds S[row l%16][keys 16kb + 4q + r], r < 4.
+//   softmax         each lane owns one query row: running max / sum in fp32,
+//                   cross-lane reductions over the 4 lane groups only.
+//   O^T += V^T . P^T  B = P^T straight from the S registers (the 32 keys of a
+//                   chunk are enumerated in the order the lanes hold them,
+//                   A = V^T read from LDS in that same order), so P never
+//                   leaves registers; lane l holds O[row l%16][dims 16db + 4q + r].
+// Scores and the softmax state are fp32; P is rounded to the cache dtype for
+// the second MFMA, as flash-attention kernels do.
+
+#include <algorithm>
+
+#include "nc_kv_common.hpp"
+#include "nc_kv_internal.hpp"
+
+namespace nckv {
+
+namespace {
+
+constexpr int kChunkWaves = 4;
+constexpr int kRows = 64;        // (query, head) rows per workgroup
+constexpr int kBN = 64;          // keys per tile
+constexpr float kNegBigC = -1.0e30f;
+constexpr int kXcdsC = 8;
+
+struct ChunkParams {
+  const void* q;
+  void* out;
+  const char* kc;
+  const char* vc;
+  const int32_t* seqlens;
+  int64_t q_sb, q_st, q_sh;
+  int64_t kc_sb, kc_st, kc_sh;
+  int64_t vc_sb, vc_st, vc_sh;
+  int32_t t_new, t_max, n_heads, n_kv_heads, group, n_hblocks;
+  int32_t n_qtiles;
+  int64_t n_groups;  // B * n_kv_heads * n_hblocks
+  int32_t window;
+  float scale_log2;
+};
+
+template <typename TC> struct mfma_t;
+template <> struct mfma_t<bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static void run(const v8& a, const v8& b, float4& c) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 acc = {c.x, c.y, c.z, c.w};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+    c = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  }
+  __device__ __forceinline__ static uint16_t from_float(float x) { return f32_to_bf16_rne(x); }
+};
+template <> struct mfma_t<f16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ __forceinline__ static void run(const v8& a, const v8& b, float4& c) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 acc = {c.x, c.y, c.z, c.w};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+    c = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  }
+  __device__ __forceinline__ static uint16_t from_float(float x) { return f32_to_f16_rne(x); }
+};
+
+template <typename TC, int D, int GB>
+__global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const ChunkParams p) {
+  typedef typename mfma_t<TC>::v8 v8;
+  constexpr int QB = kRows / GB;          // queries per workgroup
+  constexpr int DC = D / 32;              // 32-dim chunks (MFMA K for S)
+  constexpr int DB = D / 16;              // 16-dim output blocks
+  constexpr int KROW = D * 2 + 16;        // bytes per K row in LDS (padded)
+  constexpr int VROW = kBN * 2 + 8;       // bytes per V^T row in LDS (padded)
+  constexpr int CHUNKS = kBN * D / 8;     // 16-byte chunks per tile (K or V)
+  constexpr int PER_THREAD = CHUNKS / (kChunkWaves * kWave);
+  static_assert(PER_THREAD * kChunkWaves * kWave == CHUNKS, "tile / workgroup shape");
+
+  __shared__ __attribute__((aligned(16))) char ks[kBN * KROW];
+  __shared__ __attribute__((aligned(16))) char vts[D * VROW];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = tid / kWave;
+  const int lq = lane / 16;               // lane group 0..3
+  const int lr = lane % 16;
+
+  // ---- block -> (group = (b, kv head, head block), q tile); q tiles of a group share an XCD ----
+  const int64_t pb = blockIdx.x;
+  const int64_t pr = pb / kXcdsC;
+  const int qt = static_cast<int>(pr % p.n_qtiles);
+  const int64_t group = (pr / p.n_qtiles) * kXcdsC + pb % kXcdsC;
+  if (group >= p.n_groups) return;
+  int64_t gtmp = group;
+  const int hb = static_cast<int>(gtmp % p.n_hblocks); gtmp /= p.n_hblocks;
+  const int hk = static_cast<int>(gtmp % p.n_kv_heads);
+  const int64_t b = gtmp / p.n_kv_heads;
+
+  const int s = p.seqlens[b];
+  const int q0 = qt * QB;
+  const int q_end = min(q0 + QB, p.t_new);
+
+  // this lane's query row
+  const int row = wave * 16 + lr;
+  const int qi = q0 + row / GB;
+  const int h = hk * p.group + hb * GB + row % GB;
+  const bool row_ok = qi < p.t_new;
+  const int qpos = s + qi;
+  const int row_lo = p.window >= 0 ? max(0, qpos - p.window) : 0;
+
+  // keys needed by the workgroup: [lo, hi)
+  const int lo = p.window >= 0 ? max(0, s + q0 - p.window) : 0;
+  const int hi = min(s + q_end, p.t_max);
+
+  // ---- Q^T fragments (B operand): lane holds Q[row][32c + 8*lq + e] ----
+  v8 qf[DC];
+  {
+    const TC* qp = reinterpret_cast<const TC*>(static_cast<const char*>(p.q) +
+                                              (b * p.q_sb + static_cast<int64_t>(qi) * p.q_st + h * p.q_sh) *
+                                                  elem<TC>::kBytes);
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      uint4 w = make_uint4(0, 0, 0, 0);
+      if (row_ok) w = *reinterpret_cast<const uint4*>(qp + 32 * c + 8 * lq);
+      qf[c] = __builtin_bit_cast(v8, w);
+    }
+  }
+
+  float m_run = kNegBigC, l_run = 0.0f;
+  float4 acc_o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc_o[db] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+  const char* kbase = p.kc + (b * p.kc_sb + hk * p.kc_sh) * elem<TC>::kBytes;
+  const char* vbase = p.vc + (b * p.vc_sb + hk * p.vc_sh) * elem<TC>::kBytes;
+  const int64_t kst = p.kc_st * elem<TC>::kBytes;
+  const int64_t vst = p.vc_st * elem<TC>::kBytes;
+
+  for (int kt0 = lo; kt0 < hi; kt0 += kBN) {
+    // ---- stage the K tile ([key][dim]) and the V tile transposed ([dim][key]) ----
+    uint4 kreg[PER_THREAD], vreg[PER_THREAD];
+#pragma unroll
+    for (int u = 0; u < PER_THREAD; ++u) {
+      const int c = tid + u * kChunkWaves * kWave;
+      const int key = c / (D / 8);
+      const int dc = c % (D / 8);
+      const int j = kt0 + key;
+      if (j < hi) {
+        kreg[u] = *reinterpret_cast<const uint4*>(kbase + j * kst + dc * 16);
+        vreg[u] = *reinterpret_cast<const uint4*>(vbase + j * vst + dc * 16);
+      } else {
+        kreg[u] = make_uint4(0, 0, 0, 0);
+        vreg[u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    __syncthreads();  // previous tile's LDS reads are done
+#pragma unroll
+    for (int u = 0; u < PER_THREAD; ++u) {
+      const int c = tid + u * kChunkWaves * kWave;
+      const int key = c / (D / 8);
+      const int dc = c % (D / 8);
+      *reinterpret_cast<uint4*>(ks + key * KROW + dc * 16) = kreg[u];
+      const uint32_t w[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t val = static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+        *reinterpret_cast<uint16_t*>(vts + (dc * 8 + e) * VROW + key * 2) = val;
+      }
+    }
+    __syncthreads();
+
+    // ---- S^T = K . Q^T for the 4 key blocks of the tile ----
+    float4 acc_s[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      acc_s[kb] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int c = 0; c < DC; ++c) {
+        const uint4 a = *reinterpret_cast<const uint4*>(ks + (16 * kb + lr) * KROW + (32 * c + 8 * lq) * 2);
+        mfma_t<TC>::run(__builtin_bit_cast(v8, a), qf[c], acc_s[kb]);
+      }
+    }
+
+    // ---- mask, scale, online softmax (each lane: one query row) ----
+    float sv[4][4];
+    float mt = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const float a4[4] = {acc_s[kb].x, acc_s[kb].y, acc_s[kb].z, acc_s[kb].w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = kt0 + 16 * kb + 4 * lq + r;
+        const bool ok = row_ok && j >= row_lo && j <= qpos && j < hi;
+        sv[kb][r] = ok ? a4[r] * p.scale_log2 : -__builtin_inff();
+        mt = fmaxf(mt, sv[kb][r]);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = fast_exp2(m_run - m_new);
+    float rs = 0.0f;
+    uint32_t pk[4][2];  // P packed in the cache dtype: [key block][pair of r]
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      uint16_t ph[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pv = fast_exp2(sv[kb][r] - m_new);
+        rs += pv;
+        ph[r] = mfma_t<TC>::from_float(pv);
+      }
+      pk[kb][0] = static_cast<uint32_t>(ph[0]) | (static_cast<uint32_t>(ph[1]) << 16);
+      pk[kb][1] = static_cast<uint32_t>(ph[2]) | (static_cast<uint32_t>(ph[3]) << 16);
+    }
+    rs += __shfl_xor(rs, 16, kWave);
+    rs += __shfl_xor(rs, 32, kWave);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      acc_o[db].x *= alpha; acc_o[db].y *= alpha; acc_o[db].z *= alpha; acc_o[db].w *= alpha;
+    }
+
+    // ---- O^T += V^T . P^T over the two 32-key chunks ----
+#pragma unroll
+    for (int kc = 0; kc < 2; ++kc) {
+      const v8 bp = __builtin_bit_cast(v8, make_uint4(pk[2 * kc][0], pk[2 * kc][1], pk[2 * kc + 1][0], pk[2 * kc + 1][1]));
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const char* vrow = vts + (16 * db + lr) * VROW;
+        const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + (32 * kc + 4 * lq) * 2);
+        const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + (32 * kc + 16 + 4 * lq) * 2);
+        const v8 av = __builtin_bit_cast(v8, make_uint4(lo4.x, lo4.y, hi4.x, hi4.y));
+        mfma_t<TC>::run(av, bp, acc_o[db]);
+      }
+    }
+  }
+
+  // ---- normalise and store: lane holds O[row][16db + 4lq + r] ----
+  if (!row_ok) return;
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + ((b * p.t_new + qi) * p.n_heads + h) * static_cast<int64_t>(D);
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const float o4[4] = {acc_o[db].x * inv, acc_o[db].y * inv, acc_o[db].z * inv, acc_o[db].w * inv};
+    uint2 w;
+    w.x = static_cast<uint32_t>(mfma_t<TC>::from_float(o4[0])) | (static_cast<uint32_t>(mfma_t<TC>::from_float(o4[1])) << 16);
+    w.y = static_cast<uint32_t>(mfma_t<TC>::from_float(o4[2])) | (static_cast<uint32_t>(mfma_t<TC>::from_float(o4[3])) << 16);
+    *reinterpret_cast<uint2*>(op + 16 * db + 4 * lq) = w;
+  }
+}
+
+template <typename TC, int D>
+hipError_t launch_c(const ChunkParams& p, int gb, hipStream_t stream) {
+  const int64_t n_wg = kXcdsC * p.n_qtiles * ((p.n_groups + kXcdsC - 1) / kXcdsC);
+  const dim3 grid(static_cast<unsigned>(n_wg)), block(kChunkWaves * kWave);
+  switch (gb) {
+    case 8: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 8>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 4>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 2>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 1>), grid, block, 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool chunk_supports(const nc_attn_args& a) {
+  return a.t_new > 1 && a.q_dtype == a.cache_dtype &&
+         (a.cache_dtype == NC_DTYPE_BF16 || a.cache_dtype == NC_DTYPE_F16) &&
+         (a.head_dim == 64 || a.head_dim == 128);
+}
+
+int64_t chunk_grid(const nc_attn_args& a, const AttnPlan& plan) {
+  const int qb = kRows / plan.head_block;
+  const int64_t n_qtiles = (a.t_new + qb - 1) / qb;
+  const int64_t n_groups = a.batch * a.n_kv_heads * plan.n_hblocks;
+  return kXcdsC * n_qtiles * ((n_groups + kXcdsC - 1) / kXcdsC);
+}
+
+hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, hipStream_t stream) {
+  ChunkParams p;
+  p.q = a.q; p.out = a.out;
+  p.kc = static_cast<const char*>(a.k_cache); p.vc = static_cast<const char*>(a.v_cache);
+  p.seqlens = a.cache_seqlens;
+  p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
+  p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
+  p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
+  p.t_new = static_cast<int32_t>(a.t_new);
+  p.t_max = static_cast<int32_t>(a.t_max);
+  p.n_heads = static_cast<int32_t>(a.n_heads);
+  p.n_kv_heads = static_cast<int32_t>(a.n_kv_heads);
+  p.group = plan.group;
+  p.n_hblocks = plan.n_hblocks;
+  const int qb = kRows / plan.head_block;
+  p.n_qtiles = static_cast<int32_t>((a.t_new + qb - 1) / qb);
+  p.n_groups = a.batch * a.n_kv_heads * plan.n_hblocks;
+  p.window = a.window_left;
+  p.scale_log2 = a.softmax_scale * 1.4426950408889634f;
+  if (a.cache_dtype == NC_DTYPE_BF16) {
+    return a.head_dim == 64 ? launch_c<bf16, 64>(p, plan.head_block, stream)
+                            : launch_c<bf16, 128>(p, plan.head_block, stream);
+  }
+  return a.head_dim == 64 ? launch_c<f16, 64>(p, plan.head_block, stream)
+                          : launch_c<f16, 128>(p, plan.head_block, stream);
+}
+
+}  // namespace nckv

@@ -12,6 +12,9 @@ namespace nckv {
 
 namespace {
 
+// Chunks of at least this many new tokens run on the MFMA chunk kernel.
+constexpr int64_t kChunkMinTokens = 8;
+
 bool valid_dtype(int d) { return d == NC_DTYPE_F32 || d == NC_DTYPE_F16 || d == NC_DTYPE_BF16; }
 int64_t dtype_bytes(int d) { return d == NC_DTYPE_F32 ? 4 : 2; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -62,7 +65,8 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   plan->n_wg = decode_grid(plan->n_groups, plan->num_splits);
   if (plan->n_groups <= 0 || plan->n_wg <= 0 || plan->n_wg > INT32_MAX) return NC_ERR_BAD_SHAPE;
 
-  if (ns > 1) {
+  plan->use_chunk = a.t_new >= kChunkMinTokens && chunk_supports(a);
+  if (ns > 1 && !plan->use_chunk) {
     const size_t pairs = static_cast<size_t>(a.batch * a.t_new * a.n_heads);
     plan->ml_bytes = round256(pairs * ns * 2 * 4);
     plan->o_bytes = round256(pairs * ns * static_cast<size_t>(a.head_dim) * 4);
@@ -201,6 +205,7 @@ int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
       if (launch_append(ap, hs) != hipSuccess) return NC_ERR_LAUNCH;
     }
   }
+  if (plan.use_chunk) return launch_chunk(a, plan, hs) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
   return launch_decode(a, plan, s, fused, hs) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
 }
 

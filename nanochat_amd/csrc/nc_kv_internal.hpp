@@ -25,6 +25,7 @@ struct AttnPlan {
   int keys_per_split;
   int num_splits;
   int64_t n_wg;        // decode grid size
+  bool use_chunk;      // T_new > 1 on the MFMA chunk kernel (no workspace)
   size_t ml_bytes, o_bytes, total_bytes;
 };
 
@@ -37,6 +38,8 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
                          bool fused_append, hipStream_t stream);
 
 bool decode_supports(int cache_dtype, int64_t head_dim);
+bool chunk_supports(const nc_attn_args& a);
+hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, hipStream_t stream);
 int max_splits();
 int default_split_bytes();
 int64_t decode_grid(int64_t n_groups, int num_splits);

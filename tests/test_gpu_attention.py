@@ -213,3 +213,23 @@ def test_mismatched_dtypes_raise():
         q2 = torch.zeros(1, 1, 4, 48, dtype=torch.bfloat16, device=DEV)
         kc2 = torch.zeros(1, 8, 4, 48, dtype=torch.bfloat16, device=DEV)
         flash_attn.flash_attn_with_kvcache(q2, kc2, kc2.clone(), cache_seqlens=sl)
+
+
+# ---- MFMA chunk kernel (T_new >= 8, bf16/fp16 caches, head_dim 64/128) ----
+@pytest.mark.parametrize("T_new,H,H_kv,D,seqlens,window,dtype", [
+    (8, 4, 4, 128, [0, 50], -1, torch.bfloat16),             # threshold, one q tile
+    (70, 6, 6, 128, [0, 130], -1, torch.bfloat16),           # partial second q tile
+    (64, 16, 4, 128, [0, 333, 1000, 1900], -1, torch.bfloat16),  # C5-like GQA 4:1 chunk rows
+    (128, 16, 2, 64, [5, 700], 100, torch.bfloat16),         # GQA 8:1, window
+    (96, 8, 8, 128, [0, 64], 31, torch.float16),             # fp16, small window
+    (40, 12, 4, 64, [17, 0, 250], -1, torch.float16),        # GQA 3:1 (head blocks of 1)
+])
+def test_mfma_chunk_matches_oracle(T_new, H, H_kv, D, seqlens, window, dtype):
+    T_max = max(seqlens) + T_new + 3
+    _check(200 + T_new, len(seqlens), T_new, H, H_kv, D, T_max, seqlens, window, q_dtype=dtype, cache_dtype=dtype)
+
+
+@pytest.mark.parametrize("window", [-1, 512])
+def test_mfma_chunk_c3_prefill(window):
+    """C3 prefill shape: one row, 1024 tokens into an empty cache, 12 heads x 128 (S and L windows)."""
+    _check(210, 1, 1024, 12, 12, 128, 1152, [0], window)
