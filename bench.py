@@ -131,6 +131,197 @@ def cpu_baseline(budget_s: float) -> dict:
     }
 
 
+# ---------------------------------------------------------------------------
+# Further BASELINE.json configs (python bench.py --config c3|c4|c5): one JSON
+# line each with per-phase figures.  The default run (c2) is the metric line.
+# ---------------------------------------------------------------------------
+def _graph_time(stream, body, reset, reps=1):
+    """Capture body() in a HIP graph (after one eager run), time `reps` replays with HIP events."""
+    with torch.cuda.stream(stream):
+        body()
+        reset()
+        stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        body()
+    with torch.cuda.stream(stream):
+        reset()
+        graph.replay()
+        reset()
+        stream.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        stream.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def _kv_bytes(seqlens, windows, h_kv, h, d, e=2):
+    """Decode-step algorithmic bytes (same rule as step_bytes) for per-layer windows."""
+    kv_tok, qo = 2 * h_kv * d * e, 2 * h * d * e
+    total = 0
+    for w in windows:
+        for s in seqlens:
+            s = int(s)
+            n = s + 1 if w < 0 else min(s + 1, w + 1)
+            total += kv_tok * n + kv_tok + qo
+    return total
+
+
+def run_c4(dev, stream, steps):
+    """d26 SSSL decode: 26 layers, 13/13 x 128, S=1024 x19 / L=4096 x7, B=8, s=3072, `steps` tokens."""
+    from nanochat_amd.flash_attention import flash_attn_with_kvcache
+    from nanochat_amd.gpt import GPTConfig, window_sizes
+    L, H, D, B, T, S0 = 26, 13, 128, 8, 4096, 3072
+    windows = [w for w, _ in window_sizes(GPTConfig(sequence_len=4096, n_layer=L, window_pattern="SSSL"))]
+    with torch.cuda.stream(stream):
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        kc = torch.randn((L, B, T, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        vc = torch.randn_like(kc)
+        qs = torch.randn((steps, L, B, 1, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        ks, vs = torch.randn_like(qs), torch.randn_like(qs)
+        sl = torch.full((B,), S0, dtype=torch.int32, device=dev)
+
+    def body():
+        for i in range(steps):
+            for layer in range(L):
+                flash_attn_with_kvcache(qs[i, layer], kc[layer], vc[layer], k=ks[i, layer], v=vs[i, layer],
+                                        cache_seqlens=sl, causal=True, window_size=(windows[layer], 0))
+            sl.add_(1)
+
+    ms = _graph_time(stream, body, lambda: sl.fill_(S0))
+    total = sum(_kv_bytes([S0 + i] * B, windows, H, H, D) for i in range(steps))
+    gbps = total / (ms * 1e-3) / 1e9
+    return {"config": "c4", "workload": "d26 SSSL decode, 26 layers (S=1024 x19, L=4096 x7), 13/13 heads x 128, "
+                                        f"B=8, s0=3072, {steps} steps", "ms_per_step": round(ms / steps, 5),
+            "GB_per_s": round(gbps, 1), "pct_of_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+            "tokens_per_s": round(B * steps / (ms * 1e-3), 1)}
+
+
+def run_c5(dev, stream, steps):
+    """GQA mixed batch: 32 layers, 16 q / 4 kv x 128, B=64, Zipf(1.2) lengths; rows 0-47 decode,
+    rows 48-63 chunk-append 128 tokens each step (two calls per layer on row-slice views)."""
+    import numpy as np
+    from nanochat_amd.flash_attention import flash_attn_with_kvcache
+    L, H, HKV, D, B, T, C, ND = 32, 16, 4, 128, 64, 16384, 128, 48
+    hi = T - C * steps
+    rs = np.random.RandomState(0)
+    s0 = torch.tensor(np.clip(rs.zipf(1.2, B), 128, hi), dtype=torch.int32)
+    with torch.cuda.stream(stream):
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        kc = torch.empty((L, B, T, HKV, D), device=dev, dtype=torch.bfloat16).normal_(generator=g)
+        vc = torch.empty_like(kc).normal_(generator=g)
+        qd = torch.randn((steps, L, ND, 1, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        kd, vd = (torch.randn((steps, L, ND, 1, HKV, D), generator=g, device=dev, dtype=torch.bfloat16)
+                  for _ in range(2))
+        qc = torch.randn((steps, L, B - ND, C, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        kch, vch = (torch.randn((steps, L, B - ND, C, HKV, D), generator=g, device=dev, dtype=torch.bfloat16)
+                    for _ in range(2))
+        sl = s0.to(dev)
+        s0d = s0.to(dev)
+
+    def dec_body():
+        for i in range(steps):
+            for layer in range(L):
+                flash_attn_with_kvcache(qd[i, layer], kc[layer, :ND], vc[layer, :ND], k=kd[i, layer], v=vd[i, layer],
+                                        cache_seqlens=sl[:ND], causal=True, window_size=(-1, 0))
+            sl[:ND].add_(1)
+
+    def chunk_body():
+        for i in range(steps):
+            for layer in range(L):
+                flash_attn_with_kvcache(qc[i, layer], kc[layer, ND:], vc[layer, ND:], k=kch[i, layer],
+                                        v=vch[i, layer], cache_seqlens=sl[ND:], causal=True, window_size=(-1, 0))
+            sl[ND:].add_(C)
+
+    reset = lambda: sl.copy_(s0d)  # noqa: E731
+    ms_dec = _graph_time(stream, dec_body, reset)
+    ms_chunk = _graph_time(stream, chunk_body, reset)
+    dec_bytes = sum(_kv_bytes((s0[:ND] + i).tolist(), [-1] * L, HKV, H, D) for i in range(steps))
+    flops = 0
+    for i in range(steps):
+        for s in (s0[ND:] + C * i).tolist():
+            flops += L * 4 * H * D * sum(s + j + 1 for j in range(C))
+    gbps = dec_bytes / (ms_dec * 1e-3) / 1e9
+    tflops = flops / (ms_chunk * 1e-3) / 1e12
+    return {"config": "c5", "workload": f"GQA mixed: 32 layers, 16q/4kv x 128, B=64 (48 decode + 16 x 128-token "
+                                        f"chunks), Zipf(1.2) lengths in [128, {hi}], {steps} steps",
+            "decode_ms_per_step": round(ms_dec / steps, 4), "decode_GB_per_s": round(gbps, 1),
+            "decode_pct_of_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+            "chunk_ms_per_step": round(ms_chunk / steps, 4), "chunk_TFLOP_per_s": round(tflops, 1),
+            "chunk_pct_of_bf16_peak": round(100 * tflops / 2500.0, 2),
+            "step_ms": round((ms_dec + ms_chunk) / steps, 4), "seqlens_mean": float(s0.float().mean())}
+
+
+def run_c3(dev, stream, steps):
+    """d24 kernel twin: 1024-token chunk prefill into one row (24 layers, SSSL at seq 2048), fan-out to
+    16 rows of 1152, then `steps` decode steps of the 16 rows."""
+    import ctypes
+    from nanochat_amd import _ext
+    from nanochat_amd.engine import KVCache
+    from nanochat_amd.flash_attention import flash_attn_with_kvcache
+    from nanochat_amd.gpt import GPTConfig, window_sizes
+    L, H, D, P, N = 24, 12, 128, 1024, 16
+    windows = [w for w, _ in window_sizes(GPTConfig(sequence_len=2048, n_layer=L, window_pattern="SSSL"))]
+    with torch.cuda.stream(stream):
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        src = KVCache(1, H, P, D, L, dev, torch.bfloat16)
+        qp = torch.randn((L, 1, P, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        kp, vp = torch.randn_like(qp), torch.randn_like(qp)
+        dst = KVCache(N, H, P + 128, D, L, dev, torch.bfloat16)
+        qd = torch.randn((steps, L, N, 1, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        kd, vd = torch.randn_like(qd), torch.randn_like(qd)
+
+    def prefill_body():
+        for layer in range(L):
+            flash_attn_with_kvcache(qp[layer], src.k_cache[layer], src.v_cache[layer], k=kp[layer], v=vp[layer],
+                                    cache_seqlens=src.cache_seqlens, causal=True, window_size=(windows[layer], 0))
+        src.cache_seqlens.add_(P)
+
+    ms_prefill = _graph_time(stream, prefill_body, lambda: src.cache_seqlens.zero_(), reps=5)
+    a = _ext.FanoutArgs()
+    a.k_src, a.v_src = src.k_cache.data_ptr(), src.v_cache.data_ptr()
+    a.k_dst, a.v_dst = dst.k_cache.data_ptr(), dst.v_cache.data_ptr()
+    a.dst_seqlens = dst.cache_seqlens.data_ptr()
+    a.n_layers, a.n_rows, a.prefix_len, a.row_elems = L, N, P, H * D
+    a.src_stride_l, a.dst_stride_l, a.dst_stride_b = src.k_cache.stride(0), dst.k_cache.stride(0), dst.k_cache.stride(1)
+    a.dtype = 2
+
+    def fanout_body():
+        _ext.check(_ext.lib().nc_kv_fanout(ctypes.byref(a), torch.cuda.current_stream().cuda_stream), "fanout")
+
+    ms_fan = _graph_time(stream, fanout_body, lambda: None, reps=10)
+
+    def decode_body():
+        for i in range(steps):
+            for layer in range(L):
+                flash_attn_with_kvcache(qd[i, layer], dst.k_cache[layer], dst.v_cache[layer], k=kd[i, layer],
+                                        v=vd[i, layer], cache_seqlens=dst.cache_seqlens, causal=True,
+                                        window_size=(windows[layer], 0))
+            dst.cache_seqlens.add_(1)
+
+    ms_dec = _graph_time(stream, decode_body, lambda: dst.cache_seqlens.fill_(P))
+    flops = 0
+    for w in windows:
+        flops += 4 * H * D * sum(min(i + 1, w + 1) for i in range(P))
+    fan_bytes = L * 2 * P * H * D * 2 * (1 + N)
+    dec_bytes = sum(_kv_bytes([P + i] * N, windows, H, H, D) for i in range(steps))
+    return {"config": "c3", "workload": f"d24: prefill 1024 tokens (24 layers, SSSL S=512/L=2048, 12 heads x 128) "
+                                        f"-> fan-out to 16 rows of 1152 -> {steps} decode steps",
+            "prefill_ms": round(ms_prefill, 4), "prefill_TFLOP_per_s": round(flops / (ms_prefill * 1e-3) / 1e12, 1),
+            "prefill_pct_of_bf16_peak": round(100 * flops / (ms_prefill * 1e-3) / 2.5e15, 2),
+            "prefill_GFLOP": round(flops / 1e9, 2),
+            "fanout_ms": round(ms_fan, 4), "fanout_GB_per_s": round(fan_bytes / (ms_fan * 1e-3) / 1e9, 1),
+            "fanout_pct_of_peak": round(100 * fan_bytes / (ms_fan * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
+            "decode_ms_per_step": round(ms_dec / steps, 4),
+            "decode_GB_per_s": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,12 +330,24 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--keys-per-split", type=int, default=0)
     ap.add_argument("--eager", action="store_true", help="also time the steps without a graph")
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"],
+                    help="c2 (default) is the metric line; c3/c4/c5 print per-phase figures")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the KV-cache path has no cross-GPU part); "
               "run with --gpus 1", file=sys.stderr)
         return 2
+    if args.config != "c2":
+        from nanochat_amd import _ext
+        _ext.lib()
+        dev = torch.device("cuda", 0)
+        torch.cuda.set_device(dev)
+        stream = torch.cuda.Stream(device=dev)
+        runner = {"c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config]
+        steps = {"c3": min(args.steps, 128), "c4": min(args.steps, 256), "c5": min(args.steps, 16)}[args.config]
+        print(json.dumps(runner(dev, stream, steps)), flush=True)
+        return 0
     if args.steps < 1 or args.steps > T_MAX - S_HI:
         print(f"bench.py: --steps must be in [1, {T_MAX - S_HI}] (cache capacity {T_MAX})", file=sys.stderr)
         return 2

@@ -55,6 +55,12 @@
 #ifndef NC_DECODE_NT_LOADS
 #define NC_DECODE_NT_LOADS 1    // 1: K/V loads carry the non-temporal hint (+12% measured)
 #endif
+#ifndef NC_DECODE_PIPELINE
+#define NC_DECODE_PIPELINE 0    // 1: the next tile's loads are issued before the current tile is consumed
+#endif
+#ifndef NC_DECODE_EVEN_SPLITS
+#define NC_DECODE_EVEN_SPLITS 0 // 1: every split of a row gets ceil(n / num_splits) keys (no empty splits)
+#endif
 #ifndef NC_DECODE_KEY_BYTES
 #define NC_DECODE_KEY_BYTES 65536  // default split: this many K bytes per unit (and as many V)
 #endif
@@ -146,7 +152,7 @@ __device__ __forceinline__ uint4 load16(const char* p) {
 
 // Key range [lo, hi) of query t of row b and its split count.
 struct KeyRange {
-  int qpos, lo, hi, n, nsplit;
+  int qpos, lo, hi, n, nsplit, kps;
 };
 
 __device__ __forceinline__ KeyRange key_range(const DecodeParams& p, int64_t b, int t) {
@@ -155,7 +161,12 @@ __device__ __forceinline__ KeyRange key_range(const DecodeParams& p, int64_t b, 
   r.hi = min(r.qpos + 1, p.t_max);
   r.lo = p.window >= 0 ? max(0, r.qpos - p.window) : 0;
   r.n = r.hi - r.lo;
-  r.nsplit = r.n > 0 ? (r.n + p.keys_per_split - 1) / p.keys_per_split : 1;
+#if NC_DECODE_EVEN_SPLITS
+  r.kps = r.n > 0 ? ((r.n + p.num_splits - 1) / p.num_splits + 15) / 16 * 16 : p.keys_per_split;
+#else
+  r.kps = p.keys_per_split;
+#endif
+  r.nsplit = r.n > 0 ? (r.n + r.kps - 1) / r.kps : 1;
   return r;
 }
 
@@ -273,8 +284,8 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
     return;
   }
   const int qpos = kr.qpos;
-  const int k0 = kr.lo + split * p.keys_per_split;
-  const int k1 = kr.n > 0 ? min(k0 + p.keys_per_split, kr.hi) : k0;
+  const int k0 = kr.lo + split * kr.kps;
+  const int k1 = kr.n > 0 ? min(k0 + kr.kps, kr.hi) : k0;
   const bool new_in_range = p.fused && qpos >= 0 && qpos < p.t_max;
   const bool own_new = new_in_range && kr.n > 0 && k1 == qpos + 1;
   const int kc_end = own_new ? k1 - 1 : k1;       // keys read from the cache: [k0, kc_end)
@@ -314,8 +325,7 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
   const int64_t vst = p.vc_st * EB;
 
   // ---- stream the split's cache keys, TILE keys per wave per step ----
-  for (int base = k0 + wave * TILE; base < kc_end; base += NW * TILE) {
-    uint4 kv[NI], vv[NI];
+  auto load_tile = [&](int base, uint4 (&kv)[NI], uint4 (&vv)[NI]) {
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int j = base + i * KPI + row;
@@ -327,6 +337,8 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
         vv[i] = make_uint4(0, 0, 0, 0);
       }
     }
+  };
+  auto consume_tile = [&](int base, const uint4 (&kv)[NI], const uint4 (&vv)[NI]) {
     float sc[GB][NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
@@ -361,7 +373,31 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
         for (int e = 0; e < VEC; ++e) o[g][e] = __builtin_fmaf(pr, vf[e], o[g][e]);
       }
     }
+  };
+  constexpr int STEP = NW * TILE;
+#if NC_DECODE_PIPELINE
+  {
+    // two register buffers; the loads of the next tile are in flight while this one is consumed
+    uint4 ka[NI], va[NI], kb2[NI], vb2[NI];
+    int base = k0 + wave * TILE;
+    if (base < kc_end) load_tile(base, ka, va);
+    while (base < kc_end) {
+      if (base + STEP < kc_end) load_tile(base + STEP, kb2, vb2);
+      consume_tile(base, ka, va);
+      base += STEP;
+      if (base >= kc_end) break;
+      if (base + STEP < kc_end) load_tile(base + STEP, ka, va);
+      consume_tile(base, kb2, vb2);
+      base += STEP;
+    }
   }
+#else
+  for (int base = k0 + wave * TILE; base < kc_end; base += STEP) {
+    uint4 kv[NI], vv[NI];
+    load_tile(base, kv, vv);
+    consume_tile(base, kv, vv);
+  }
+#endif
 
   // ---- the appended token (fused path): read from k/v, store into the cache ----
   if (own_new && wave == NW - 1) {
