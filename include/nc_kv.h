@@ -139,7 +139,8 @@ typedef struct nc_attn_args {
   float softmax_scale;           /* nanochat: head_dim ** -0.5 */
   int32_t q_dtype;               /* dtype of q, k, v and out */
   int32_t cache_dtype;
-  int32_t keys_per_split;        /* 0: library default; else a multiple of 64 */
+  int32_t keys_per_split;        /* keys one workgroup covers before a split-K merge;
+                                    0: library default; else a multiple of 64 */
 } nc_attn_args;
 
 /* Bytes of workspace nc_attn_kvcache needs for these arguments. */

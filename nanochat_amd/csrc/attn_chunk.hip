@@ -6,8 +6,8 @@
 // Tiling.  A workgroup owns 64 "rows" = (query, q head) pairs of one
 // (row b, kv head, q-head block): 64 / GB queries x GB heads, so the GB heads
 // that share a kv head read each K/V tile once.  4 waves x 16 rows.  Key tiles
-// of 64 positions are staged in LDS: K as [key][dim] and V transposed as
-// [dim][key], both padded so the MFMA operand reads are bank-conflict free.
+// of 64 positions are staged in LDS as [key][dim] rows (16-byte stores), padded
+// so the MFMA operand reads are bank-conflict free.
 //
 // Per tile and wave (v_mfma_f32_16x16x32_{bf16,f16}; lane l, q = l / 16):
 //   S^T = K . Q^T   A = K[16 keys][32 dims] (LDS), B = Q^T (registers);
@@ -15,11 +15,23 @@
 //   softmax         each lane owns one query row: running max / sum in fp32,
 //                   cross-lane reductions over the 4 lane groups only.
 //   O^T += V^T . P^T  B = P^T straight from the S registers (the 32 keys of a
-//                   chunk are enumerated in the order the lanes hold them,
-//                   A = V^T read from LDS in that same order), so P never
-//                   leaves registers; lane l holds O[row l%16][dims 16db + 4q + r].
+//                   chunk are enumerated in the order the lanes hold them), so
+//                   P never leaves registers.  A = V^T in that same key order
+//                   comes from the [key][dim] LDS rows through two gfx950
+//                   transpose reads (ds_read_b64_tr_b16: in each 16-lane group,
+//                   lane i receives element i of the four 8-byte rows its
+//                   neighbours point at, i.e. 4 keys of dim i).
+//                   Lane l holds O[row l%16][dims 16db + 4q + r].
 // Scores and the softmax state are fp32; P is rounded to the cache dtype for
 // the second MFMA, as flash-attention kernels do.
+//
+// Split-K: a workgroup's key span [lo, hi) is cut into `keys_per_split`
+// pieces handled by separate workgroups, so long caches keep the chip busy.
+// A span that fits one split writes the output directly; otherwise each split
+// writes (o, m, l) partials per (query, head) and the split-merge kernel of
+// the decode path combines them (chunk_span gives both sides the same split
+// count; workgroups past it return at once).  The next key tile is
+// loaded into registers while the current one is consumed from LDS.
 
 #include <algorithm>
 
@@ -36,6 +48,15 @@ constexpr int kBN = 64;          // keys per tile
 constexpr float kNegBigC = -1.0e30f;
 constexpr int kXcdsC = 8;
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef __attribute__((address_space(3))) char lds_char;
+
+// ds_read_b64_tr_b16 from a generic pointer into a __shared__ array.
+__device__ __forceinline__ i16x4 lds_read_tr16(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((lds_char*)(p)));
+}
+
 struct ChunkParams {
   const void* q;
   void* out;
@@ -50,6 +71,9 @@ struct ChunkParams {
   int64_t n_groups;  // B * n_kv_heads * n_hblocks
   int32_t window;
   float scale_log2;
+  int32_t num_splits, keys_per_split;
+  float* part_ml;
+  float* part_o;
 };
 
 template <typename TC> struct mfma_t;
@@ -80,14 +104,14 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   constexpr int QB = kRows / GB;          // queries per workgroup
   constexpr int DC = D / 32;              // 32-dim chunks (MFMA K for S)
   constexpr int DB = D / 16;              // 16-dim output blocks
-  constexpr int KROW = D * 2 + 16;        // bytes per K row in LDS (padded)
-  constexpr int VROW = kBN * 2 + 8;       // bytes per V^T row in LDS (padded)
+  constexpr int KROW = D * 2 + 16;        // bytes per K row in LDS (padded: 16-byte reads, 8 lanes/cycle)
+  constexpr int VROW = D * 2 + 32;        // bytes per V row in LDS (padded: transpose reads, 16 lanes/cycle)
   constexpr int CHUNKS = kBN * D / 8;     // 16-byte chunks per tile (K or V)
   constexpr int PER_THREAD = CHUNKS / (kChunkWaves * kWave);
   static_assert(PER_THREAD * kChunkWaves * kWave == CHUNKS, "tile / workgroup shape");
 
   __shared__ __attribute__((aligned(16))) char ks[kBN * KROW];
-  __shared__ __attribute__((aligned(16))) char vts[D * VROW];
+  __shared__ __attribute__((aligned(16))) char vs[kBN * VROW];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -95,11 +119,14 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int lq = lane / 16;               // lane group 0..3
   const int lr = lane % 16;
 
-  // ---- block -> (group = (b, kv head, head block), q tile); q tiles of a group share an XCD ----
+  // ---- block -> (group = (b, kv head, head block), q tile, split); a group's blocks share an XCD ----
   const int64_t pb = blockIdx.x;
   const int64_t pr = pb / kXcdsC;
-  const int qt = static_cast<int>(pr % p.n_qtiles);
-  const int64_t group = (pr / p.n_qtiles) * kXcdsC + pb % kXcdsC;
+  const int members = p.n_qtiles * p.num_splits;
+  const int member = static_cast<int>(pr % members);
+  const int qt = member / p.num_splits;
+  const int split = member % p.num_splits;
+  const int64_t group = (pr / members) * kXcdsC + pb % kXcdsC;
   if (group >= p.n_groups) return;
   int64_t gtmp = group;
   const int hb = static_cast<int>(gtmp % p.n_hblocks); gtmp /= p.n_hblocks;
@@ -118,9 +145,13 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int qpos = s + qi;
   const int row_lo = p.window >= 0 ? max(0, qpos - p.window) : 0;
 
-  // keys needed by the workgroup: [lo, hi)
-  const int lo = p.window >= 0 ? max(0, s + q0 - p.window) : 0;
-  const int hi = min(s + q_end, p.t_max);
+  // keys of this split: [lo, hi) within the workgroup's span; splits past the
+  // span's own split count have nothing to do (the merge never reads them)
+  const ChunkSpan span = chunk_span(s, q0, q_end, p.t_max, p.window, p.keys_per_split);
+  if (split >= span.nsplit) return;
+  const int lo = span.lo + split * p.keys_per_split;
+  const int hi = min(span.hi, lo + p.keys_per_split);
+  const int64_t pair_row = (b * p.t_new + qi) * p.n_heads + h;  // this lane's (query, head)
 
   // ---- Q^T fragments (B operand): lane holds Q[row][32c + 8*lq + e] ----
   v8 qf[DC];
@@ -146,15 +177,14 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int64_t kst = p.kc_st * elem<TC>::kBytes;
   const int64_t vst = p.vc_st * elem<TC>::kBytes;
 
-  for (int kt0 = lo; kt0 < hi; kt0 += kBN) {
-    // ---- stage the K tile ([key][dim]) and the V tile transposed ([dim][key]) ----
-    uint4 kreg[PER_THREAD], vreg[PER_THREAD];
+  // ---- key tiles: registers hold the next tile while the current one is consumed from LDS ----
+  uint4 kreg[PER_THREAD], vreg[PER_THREAD];
+  auto load_regs = [&](int kt0) {
 #pragma unroll
     for (int u = 0; u < PER_THREAD; ++u) {
       const int c = tid + u * kChunkWaves * kWave;
-      const int key = c / (D / 8);
+      const int j = kt0 + c / (D / 8);
       const int dc = c % (D / 8);
-      const int j = kt0 + key;
       if (j < hi) {
         kreg[u] = *reinterpret_cast<const uint4*>(kbase + j * kst + dc * 16);
         vreg[u] = *reinterpret_cast<const uint4*>(vbase + j * vst + dc * 16);
@@ -163,6 +193,9 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
         vreg[u] = make_uint4(0, 0, 0, 0);
       }
     }
+  };
+  load_regs(lo);
+  for (int kt0 = lo; kt0 < hi; kt0 += kBN) {
     __syncthreads();  // previous tile's LDS reads are done
 #pragma unroll
     for (int u = 0; u < PER_THREAD; ++u) {
@@ -170,14 +203,10 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
       const int key = c / (D / 8);
       const int dc = c % (D / 8);
       *reinterpret_cast<uint4*>(ks + key * KROW + dc * 16) = kreg[u];
-      const uint32_t w[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t val = static_cast<uint16_t>((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
-        *reinterpret_cast<uint16_t*>(vts + (dc * 8 + e) * VROW + key * 2) = val;
-      }
+      *reinterpret_cast<uint4*>(vs + key * VROW + dc * 16) = vreg[u];
     }
     __syncthreads();
+    if (kt0 + kBN < hi) load_regs(kt0 + kBN);
 
     // ---- S^T = K . Q^T for the 4 key blocks of the tile ----
     float4 acc_s[4];
@@ -238,19 +267,32 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
       const v8 bp = __builtin_bit_cast(v8, make_uint4(pk[2 * kc][0], pk[2 * kc][1], pk[2 * kc + 1][0], pk[2 * kc + 1][1]));
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const char* vrow = vts + (16 * db + lr) * VROW;
-        const uint2 lo4 = *reinterpret_cast<const uint2*>(vrow + (32 * kc + 4 * lq) * 2);
-        const uint2 hi4 = *reinterpret_cast<const uint2*>(vrow + (32 * kc + 16 + 4 * lq) * 2);
-        const v8 av = __builtin_bit_cast(v8, make_uint4(lo4.x, lo4.y, hi4.x, hi4.y));
+        // lane lr of group lq points at key (base + lr/4), dims 16db + 4*(lr%4) .. +3
+        const char* src0 = vs + (32 * kc + 4 * lq + lr / 4) * VROW + (16 * db + 4 * (lr % 4)) * 2;
+        const char* src1 = src0 + 16 * VROW;
+        const i16x4 lo4 = lds_read_tr16(src0);
+        const i16x4 hi4 = lds_read_tr16(src1);
+        const uint2 a = __builtin_bit_cast(uint2, lo4), c = __builtin_bit_cast(uint2, hi4);
+        const v8 av = __builtin_bit_cast(v8, make_uint4(a.x, a.y, c.x, c.y));
         mfma_t<TC>::run(av, bp, acc_o[db]);
       }
     }
   }
 
-  // ---- normalise and store: lane holds O[row][16db + 4lq + r] ----
   if (!row_ok) return;
+  if (span.nsplit > 1) {
+    // ---- partials for the merge kernel: o unnormalised, (m, l) once per row ----
+    float* po = p.part_o + (pair_row * p.num_splits + split) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) *reinterpret_cast<float4*>(po + 16 * db + 4 * lq) = acc_o[db];
+    if (lq == 0) {
+      *reinterpret_cast<float2*>(p.part_ml + (pair_row * p.num_splits + split) * 2) = make_float2(m_run, l_run);
+    }
+    return;
+  }
+  // ---- normalise and store: lane holds O[row][16db + 4lq + r] ----
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + ((b * p.t_new + qi) * p.n_heads + h) * static_cast<int64_t>(D);
+  uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + pair_row * static_cast<int64_t>(D);
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
     const float o4[4] = {acc_o[db].x * inv, acc_o[db].y * inv, acc_o[db].z * inv, acc_o[db].w * inv};
@@ -263,7 +305,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
 
 template <typename TC, int D>
 hipError_t launch_c(const ChunkParams& p, int gb, hipStream_t stream) {
-  const int64_t n_wg = kXcdsC * p.n_qtiles * ((p.n_groups + kXcdsC - 1) / kXcdsC);
+  const int64_t n_wg = static_cast<int64_t>(kXcdsC) * p.n_qtiles * p.num_splits * ((p.n_groups + kXcdsC - 1) / kXcdsC);
   const dim3 grid(static_cast<unsigned>(n_wg)), block(kChunkWaves * kWave);
   switch (gb) {
     case 8: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 8>), grid, block, 0, stream, p); break;
@@ -282,14 +324,9 @@ bool chunk_supports(const nc_attn_args& a) {
          (a.head_dim == 64 || a.head_dim == 128);
 }
 
-int64_t chunk_grid(const nc_attn_args& a, const AttnPlan& plan) {
-  const int qb = kRows / plan.head_block;
-  const int64_t n_qtiles = (a.t_new + qb - 1) / qb;
-  const int64_t n_groups = a.batch * a.n_kv_heads * plan.n_hblocks;
-  return kXcdsC * n_qtiles * ((n_groups + kXcdsC - 1) / kXcdsC);
-}
+int chunk_rows_per_wg() { return kRows; }
 
-hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, hipStream_t stream) {
+hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream) {
   ChunkParams p;
   p.q = a.q; p.out = a.out;
   p.kc = static_cast<const char*>(a.k_cache); p.vc = static_cast<const char*>(a.v_cache);
@@ -308,6 +345,10 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, hipStream_t
   p.n_groups = a.batch * a.n_kv_heads * plan.n_hblocks;
   p.window = a.window_left;
   p.scale_log2 = a.softmax_scale * 1.4426950408889634f;
+  p.num_splits = plan.chunk_splits;
+  p.keys_per_split = plan.chunk_keys_per_split;
+  p.part_ml = s.part_ml;
+  p.part_o = s.part_o;
   if (a.cache_dtype == NC_DTYPE_BF16) {
     return a.head_dim == 64 ? launch_c<bf16, 64>(p, plan.head_block, stream)
                             : launch_c<bf16, 128>(p, plan.head_block, stream);

@@ -16,11 +16,12 @@
 //   state (max m, sum l, output o); rows are merged by a butterfly and waves
 //   through LDS once at the end.
 //
-// Split merge: when the plan has one split the decode kernel writes the output.
-// Otherwise every split writes (o, m, l) partials to the workspace (a split
-// past the end of its row writes only l = 0, which marks it empty) and
-// merge_splits_kernel, the next launch on the stream, combines all split slots
-// with the log-sum-exp rule without re-reading cache_seqlens.  The
+// Split merge: a query whose key range fits one split (always, when the plan
+// has one split) gets its output from the decode kernel directly.  Otherwise
+// each of its splits writes (o, m, l) partials to the workspace (a split past
+// the end of the range does nothing) and merge_splits_kernel, the next launch
+// on the stream, recomputes the query's split count from cache_seqlens and
+// combines exactly those slots with the log-sum-exp rule.  The
 // kernel boundary is the only synchronisation: an in-kernel "last split
 // merges" scheme needs agent-scope release fences (L2 write-back), which
 // measured 3-10x slower on MI355X.  The splits of one (b, t, unit) run on the
@@ -98,6 +99,7 @@ struct DecodeParams {
   int32_t q_dtype;
   int32_t num_splits, keys_per_split;
   int32_t fused;
+  int32_t merge_qb;  // split merge: 0 = decode splits (per query); > 0 = chunk splits (per QB-query tile)
 };
 
 template <typename TC> struct dot_packed;
@@ -190,27 +192,43 @@ __device__ __forceinline__ GroupIdx group_index(const DecodeParams& p, int64_t g
 constexpr int kMergeChunk = 16;
 
 // Second pass: block g combines the split partials of group g's GB heads.
-// Each thread owns one output element and folds the split slots in chunks of
-// 16 with all loads of a chunk in flight together, so up to 16 splits cost
-// one memory round trip; the (m, l) reads are uniform per head (one
-// transaction per wave).  Slots with l == 0 are empty and contribute nothing
-// (their o was never written).
+// The block recomputes how many splits its query's producer used (decode:
+// the query's key range; chunk: its workgroup's span) and reads exactly those
+// slots; a query with one split was written directly by its producer.  Each
+// thread owns one output element and folds the slots in chunks of 16 with
+// all loads of a chunk in flight together, so up to 16 splits cost one
+// memory round trip; the (m, l) reads are uniform per head (one transaction
+// per wave).  Slots with l == 0 (every key of the split masked for this
+// query) contribute nothing.
 template <int D, int GB>
 __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p) {
   const GroupIdx gi = group_index(p, blockIdx.x);
-  const int nsplit = p.num_splits;
+  int nsplit;
+  if (p.merge_qb == 0) {
+    nsplit = key_range(p, gi.b, gi.t).nsplit;
+  } else {
+    const int q0 = gi.t / p.merge_qb * p.merge_qb;
+    nsplit = chunk_span(p.seqlens[gi.b], q0, min(q0 + p.merge_qb, p.t_new), p.t_max, p.window,
+                        p.keys_per_split).nsplit;
+  }
+  // Decode splits with at most 16 slots: load every allocated slot without
+  // waiting for cache_seqlens (one memory round trip instead of two); slots
+  // past the query's split count hold stale data and are masked out below.
+  const bool eager = p.merge_qb == 0 && p.num_splits <= kMergeChunk;
+  if (!eager && nsplit <= 1) return;
+  const int lim = eager ? p.num_splits : nsplit;
   const int64_t pair0 = (gi.b * p.t_new + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;
   for (int idx = threadIdx.x; idx < GB * D; idx += blockDim.x) {
     const int g = idx / D, d = idx % D;
-    const float* ml = p.part_ml + (pair0 + g) * nsplit * 2;
-    const float* po = p.part_o + (pair0 + g) * nsplit * D + d;
+    const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
+    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d;
     float M = kNegBig, L = 0.0f, O = 0.0f;
-    for (int sp0 = 0; sp0 < nsplit; sp0 += kMergeChunk) {
+    for (int sp0 = 0; sp0 < lim; sp0 += kMergeChunk) {
       float ms[kMergeChunk], ls[kMergeChunk], os[kMergeChunk];
 #pragma unroll
       for (int u = 0; u < kMergeChunk; ++u) {
         const int sp = sp0 + u;
-        if (sp < nsplit) {
+        if (sp < lim) {
           const float2 v = *reinterpret_cast<const float2*>(ml + 2 * sp);
           ms[u] = v.x;
           ls[u] = v.y;
@@ -220,6 +238,10 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
           ls[u] = 0.0f;
           os[u] = 0.0f;
         }
+      }
+#pragma unroll
+      for (int u = 0; u < kMergeChunk; ++u) {
+        if (sp0 + u >= nsplit) ls[u] = 0.0f;  // slot not written by this call
       }
       float mx = M;
 #pragma unroll
@@ -235,6 +257,7 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
       }
       M = mx;
     }
+    if (nsplit <= 1) return;  // the producer wrote this query's output
     store_any(p.out, (pair0 + g) * D + d, p.q_dtype, L > 0.0f ? O / L : 0.0f);
   }
 }
@@ -279,10 +302,7 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
 
   const KeyRange kr = key_range(p, b, t);
   const int64_t pair0 = (b * p.t_new + t) * p.n_heads + hk * p.group + hb * GB;  // (b, t, first q head)
-  if (split >= kr.nsplit) {
-    if (tid < GB) p.part_ml[((pair0 + tid) * p.num_splits + split) * 2 + 1] = 0.0f;  // empty slot
-    return;
-  }
+  if (split >= kr.nsplit) return;  // past this query's keys: the merge never reads this slot
   const int qpos = kr.qpos;
   const int k0 = kr.lo + split * kr.kps;
   const int k1 = kr.n > 0 ? min(k0 + kr.kps, kr.hi) : k0;
@@ -475,7 +495,7 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
   }
   __syncthreads();
 
-  if (p.num_splits == 1) {
+  if (kr.nsplit == 1) {
     for (int idx = tid; idx < GB * D; idx += NW * kWave) {
       const int g = idx / D, d = idx % D;
       float acc = 0.0f;
@@ -550,8 +570,9 @@ int64_t decode_grid(int64_t n_groups, int num_splits) {
 #endif
 }
 
-hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
-                         bool fused_append, hipStream_t stream) {
+namespace {
+
+DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, bool fused_append) {
   DecodeParams p;
   p.q = a.q; p.out = a.out;
   p.kc = static_cast<char*>(a.k_cache); p.vc = static_cast<char*>(a.v_cache);
@@ -577,6 +598,42 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.num_splits = plan.num_splits;
   p.keys_per_split = plan.keys_per_split;
   p.fused = fused_append ? 1 : 0;
+  p.merge_qb = 0;
+  return p;
+}
+
+template <int D>
+hipError_t launch_merge_d(const DecodeParams& p, int gb, hipStream_t stream) {
+  const int threads = std::min(256, (gb * D + kWave - 1) / kWave * kWave);
+  const dim3 grid(static_cast<unsigned>(p.n_groups)), block(threads);
+  switch (gb) {
+    case 8: hipLaunchKernelGGL((merge_splits_kernel<D, 8>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((merge_splits_kernel<D, 4>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((merge_splits_kernel<D, 2>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((merge_splits_kernel<D, 1>), grid, block, 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
+                              hipStream_t stream) {
+  DecodeParams p = make_params(a, plan, s, false);
+  p.num_splits = plan.chunk_splits;
+  p.keys_per_split = plan.chunk_keys_per_split;
+  p.merge_qb = chunk_rows_per_wg() / plan.head_block;
+  switch (a.head_dim) {
+    case 32: return launch_merge_d<32>(p, plan.head_block, stream);
+    case 64: return launch_merge_d<64>(p, plan.head_block, stream);
+    case 128: return launch_merge_d<128>(p, plan.head_block, stream);
+    default: return launch_merge_d<256>(p, plan.head_block, stream);
+  }
+}
+
+hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
+                         bool fused_append, hipStream_t stream) {
+  const DecodeParams p = make_params(a, plan, s, fused_append);
   const bool qpk = a.q_dtype == a.cache_dtype && a.cache_dtype != NC_DTYPE_F32;
   const int gb = plan.head_block;
   switch (a.cache_dtype) {

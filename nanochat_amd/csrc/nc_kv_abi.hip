@@ -14,6 +14,13 @@ namespace {
 
 // Chunks of at least this many new tokens run on the MFMA chunk kernel.
 constexpr int64_t kChunkMinTokens = 8;
+// Default key span of one chunk-kernel split (8 tiles of 64 keys), used when
+// a workgroup's span can exceed kChunkSplitAbove keys.  Shorter spans run
+// unsplit: measured on MI355X, the merge launch costs more than the shorter
+// critical path saves (d24 1024-token prefill: 0.65 ms unsplit, 0.86 ms at
+// 512-key splits; a 16k-key GQA chunk batch: 7.95 ms at 512, 10.8 unsplit).
+constexpr int64_t kChunkKeysPerSplit = 512;
+constexpr int64_t kChunkSplitAbove = 2048;
 
 bool valid_dtype(int d) { return d == NC_DTYPE_F32 || d == NC_DTYPE_F16 || d == NC_DTYPE_BF16; }
 int64_t dtype_bytes(int d) { return d == NC_DTYPE_F32 ? 4 : 2; }
@@ -66,10 +73,27 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   if (plan->n_groups <= 0 || plan->n_wg <= 0 || plan->n_wg > INT32_MAX) return NC_ERR_BAD_SHAPE;
 
   plan->use_chunk = a.t_new >= kChunkMinTokens && chunk_supports(a);
-  if (ns > 1 && !plan->use_chunk) {
+  plan->chunk_keys_per_split = 0;
+  plan->chunk_splits = 1;
+  if (plan->use_chunk) {
+    // one workgroup's keys span at most (window + its queries) or the cache length
+    const int64_t qb = chunk_rows_per_wg() / hb;
+    const int64_t span = a.window_left >= 0 ? std::min<int64_t>(a.t_max, int64_t(a.window_left) + qb) : a.t_max;
+    int64_t ckps = a.keys_per_split > 0 ? a.keys_per_split
+                                        : (span > kChunkSplitAbove ? kChunkKeysPerSplit : span);
+    int64_t cns = (span + ckps - 1) / ckps;
+    if (cns > cap) {
+      ckps = ((span + cap - 1) / cap + 63) / 64 * 64;
+      cns = (span + ckps - 1) / ckps;
+    }
+    plan->chunk_keys_per_split = static_cast<int>(ckps);
+    plan->chunk_splits = static_cast<int>(cns);
+  }
+  const int64_t merge_splits = plan->use_chunk ? plan->chunk_splits : ns;
+  if (merge_splits > 1) {
     const size_t pairs = static_cast<size_t>(a.batch * a.t_new * a.n_heads);
-    plan->ml_bytes = round256(pairs * ns * 2 * 4);
-    plan->o_bytes = round256(pairs * ns * static_cast<size_t>(a.head_dim) * 4);
+    plan->ml_bytes = round256(pairs * merge_splits * 2 * 4);
+    plan->o_bytes = round256(pairs * merge_splits * static_cast<size_t>(a.head_dim) * 4);
   } else {
     plan->ml_bytes = plan->o_bytes = 0;
   }
@@ -205,7 +229,11 @@ int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
       if (launch_append(ap, hs) != hipSuccess) return NC_ERR_LAUNCH;
     }
   }
-  if (plan.use_chunk) return launch_chunk(a, plan, hs) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
+  if (plan.use_chunk) {
+    if (launch_chunk(a, plan, s, hs) != hipSuccess) return NC_ERR_LAUNCH;
+    if (plan.chunk_splits > 1 && launch_chunk_merge(a, plan, s, hs) != hipSuccess) return NC_ERR_LAUNCH;
+    return NC_OK;
+  }
   return launch_decode(a, plan, s, fused, hs) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
 }
 

@@ -163,4 +163,20 @@ __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Key span [lo, hi) of the chunk-kernel workgroup that owns queries
+// [q0, q_end) of a row whose cache held s tokens, and its split count (>= 1;
+// an empty span is one split).  The chunk kernel and the split merge both use
+// it, so they agree on which partial slots exist.
+struct ChunkSpan {
+  int lo, hi, nsplit;
+};
+
+__device__ __forceinline__ ChunkSpan chunk_span(int s, int q0, int q_end, int t_max, int window, int kps) {
+  ChunkSpan c;
+  c.lo = window >= 0 ? max(0, s + q0 - window) : 0;
+  c.hi = min(s + q_end, t_max);
+  c.nsplit = c.hi > c.lo ? (c.hi - c.lo + kps - 1) / kps : 1;
+  return c;
+}
+
 }  // namespace nckv

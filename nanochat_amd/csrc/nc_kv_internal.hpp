@@ -25,7 +25,9 @@ struct AttnPlan {
   int keys_per_split;
   int num_splits;
   int64_t n_wg;        // decode grid size
-  bool use_chunk;      // T_new > 1 on the MFMA chunk kernel (no workspace)
+  bool use_chunk;      // T_new > 1 on the MFMA chunk kernel
+  int chunk_keys_per_split;
+  int chunk_splits;    // > 1: chunk partials merged by the split-merge kernel
   size_t ml_bytes, o_bytes, total_bytes;
 };
 
@@ -39,7 +41,11 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
 
 bool decode_supports(int cache_dtype, int64_t head_dim);
 bool chunk_supports(const nc_attn_args& a);
-hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, hipStream_t stream);
+hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream);
+int chunk_rows_per_wg();
+// Split merge of the chunk kernel's partials (plan.chunk_splits > 1).
+hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
+                              hipStream_t stream);
 int max_splits();
 int default_split_bytes();
 int64_t decode_grid(int64_t n_groups, int num_splits);

@@ -233,3 +233,10 @@ def test_mfma_chunk_matches_oracle(T_new, H, H_kv, D, seqlens, window, dtype):
 def test_mfma_chunk_c3_prefill(window):
     """C3 prefill shape: one row, 1024 tokens into an empty cache, 12 heads x 128 (S and L windows)."""
     _check(210, 1, 1024, 12, 12, 128, 1152, [0], window)
+
+
+@pytest.mark.parametrize("kps,window", [(64, -1), (128, 200), (320, -1), (4096, 50)])
+def test_mfma_chunk_split_sizes(kps, window):
+    """Split-K of the chunk kernel: q tiles of one call have different split counts (ragged rows, causal
+    spans, windows); one-split tiles write directly, the others go through the merge."""
+    _check(220, 3, 100, 8, 2, 128, 1200, [0, 37, 1000], window, kps=kps)
