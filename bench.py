@@ -170,7 +170,7 @@ def _kv_bytes(seqlens, windows, h_kv, h, d, e=2):
     return total
 
 
-def run_c4(dev, stream, steps, kps=0):
+def run_c4(dev, stream, steps, kps=0, ckps=0):
     """d26 SSSL decode: 26 layers, 13/13 x 128, S=1024 x19 / L=4096 x7, B=8, s=3072, `steps` tokens."""
     from nanochat_amd.flash_attention import flash_attn_with_kvcache
     from nanochat_amd.gpt import GPTConfig, window_sizes
@@ -189,7 +189,8 @@ def run_c4(dev, stream, steps, kps=0):
         for i in range(steps):
             for layer in range(L):
                 flash_attn_with_kvcache(qs[i, layer], kc[layer], vc[layer], k=ks[i, layer], v=vs[i, layer],
-                                        cache_seqlens=sl, causal=True, window_size=(windows[layer], 0))
+                                        cache_seqlens=sl, causal=True, window_size=(windows[layer], 0),
+                                        keys_per_split=kps)
             sl.add_(1)
 
     ms = _graph_time(stream, body, lambda: sl.fill_(S0))
@@ -201,7 +202,7 @@ def run_c4(dev, stream, steps, kps=0):
             "tokens_per_s": round(B * steps / (ms * 1e-3), 1)}
 
 
-def run_c5(dev, stream, steps, kps=0):
+def run_c5(dev, stream, steps, kps=0, ckps=0):
     """GQA mixed batch: 32 layers, 16 q / 4 kv x 128, B=64, Zipf(1.2) lengths; rows 0-47 decode,
     rows 48-63 chunk-append 128 tokens each step (two calls per layer on row-slice views)."""
     import numpy as np
@@ -228,7 +229,7 @@ def run_c5(dev, stream, steps, kps=0):
         for i in range(steps):
             for layer in range(L):
                 flash_attn_with_kvcache(qd[i, layer], kc[layer, :ND], vc[layer, :ND], k=kd[i, layer], v=vd[i, layer],
-                                        cache_seqlens=sl[:ND], causal=True, window_size=(-1, 0))
+                                        cache_seqlens=sl[:ND], causal=True, window_size=(-1, 0), keys_per_split=kps)
             sl[:ND].add_(1)
 
     def chunk_body():
@@ -236,7 +237,7 @@ def run_c5(dev, stream, steps, kps=0):
             for layer in range(L):
                 flash_attn_with_kvcache(qc[i, layer], kc[layer, ND:], vc[layer, ND:], k=kch[i, layer],
                                         v=vch[i, layer], cache_seqlens=sl[ND:], causal=True, window_size=(-1, 0),
-                                        keys_per_split=kps)
+                                        keys_per_split=ckps)
             sl[ND:].add_(C)
 
     reset = lambda: sl.copy_(s0d)  # noqa: E731
@@ -258,7 +259,7 @@ def run_c5(dev, stream, steps, kps=0):
             "step_ms": round((ms_dec + ms_chunk) / steps, 4), "seqlens_mean": float(s0.float().mean())}
 
 
-def run_c3(dev, stream, steps, kps=0):
+def run_c3(dev, stream, steps, kps=0, ckps=0):
     """d24 kernel twin: 1024-token chunk prefill into one row (24 layers, SSSL at seq 2048), fan-out to
     16 rows of 1152, then `steps` decode steps of the 16 rows."""
     import ctypes
@@ -282,7 +283,7 @@ def run_c3(dev, stream, steps, kps=0):
         for layer in range(L):
             flash_attn_with_kvcache(qp[layer], src.k_cache[layer], src.v_cache[layer], k=kp[layer], v=vp[layer],
                                     cache_seqlens=src.cache_seqlens, causal=True, window_size=(windows[layer], 0),
-                                    keys_per_split=kps)
+                                    keys_per_split=ckps)
         src.cache_seqlens.add_(P)
 
     ms_prefill = _graph_time(stream, prefill_body, lambda: src.cache_seqlens.zero_(), reps=5)
@@ -304,7 +305,7 @@ def run_c3(dev, stream, steps, kps=0):
             for layer in range(L):
                 flash_attn_with_kvcache(qd[i, layer], dst.k_cache[layer], dst.v_cache[layer], k=kd[i, layer],
                                         v=vd[i, layer], cache_seqlens=dst.cache_seqlens, causal=True,
-                                        window_size=(windows[layer], 0))
+                                        window_size=(windows[layer], 0), keys_per_split=kps)
             dst.cache_seqlens.add_(1)
 
     ms_dec = _graph_time(stream, decode_body, lambda: dst.cache_seqlens.fill_(P))
@@ -330,7 +331,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--keys-per-split", type=int, default=0)
+    ap.add_argument("--keys-per-split", type=int, default=0,
+                    help="decode split size (multiple of 64; 0 = library default)")
+    ap.add_argument("--chunk-keys-per-split", type=int, default=0,
+                    help="c3/c5 chunk-kernel split size (0 = library default)")
     ap.add_argument("--eager", action="store_true", help="also time the steps without a graph")
     ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"],
                     help="c2 (default) is the metric line; c3/c4/c5 print per-phase figures")
@@ -348,7 +352,8 @@ def main() -> int:
         stream = torch.cuda.Stream(device=dev)
         runner = {"c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config]
         steps = {"c3": min(args.steps, 128), "c4": min(args.steps, 256), "c5": min(args.steps, 16)}[args.config]
-        print(json.dumps(runner(dev, stream, steps, kps=args.keys_per_split)), flush=True)
+        print(json.dumps(runner(dev, stream, steps, kps=args.keys_per_split, ckps=args.chunk_keys_per_split)),
+              flush=True)
         return 0
     if args.steps < 1 or args.steps > T_MAX - S_HI:
         print(f"bench.py: --steps must be in [1, {T_MAX - S_HI}] (cache capacity {T_MAX})", file=sys.stderr)

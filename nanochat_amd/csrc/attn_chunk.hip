@@ -1,7 +1,14 @@
 // Chunked prefill into the KV cache on MFMA (nanochat/flash_attention.py:91-102:
 // queries bottom-right aligned at s_b + i, causal, sliding window, GQA),
-// for T_new > 1 with bf16 / fp16 caches.  The new tokens are already in the
-// cache (kv_append_kernel runs first on the stream).
+// for T_new > 1 with bf16 / fp16 caches.
+//
+// Fused append: with k/v given, keys at positions >= s_b are read from k/v
+// (token j - s_b) instead of the cache, and the workgroup whose queries are
+// those tokens (head block 0, the split holding the position) also stores
+// them into the cache, so each new position is written once and no
+// workgroup of the launch reads a cache position another one writes.
+// Positions outside [0, t_max) are not stored and set NC_DEVERR_OVERFLOW,
+// as the standalone append does.
 //
 // Tiling.  A workgroup owns 64 "rows" = (query, q head) pairs of one
 // (row b, kv head, q-head block): 64 / GB queries x GB heads, so the GB heads
@@ -74,6 +81,15 @@ struct ChunkParams {
   int32_t num_splits, keys_per_split;
   float* part_ml;
   float* part_o;
+  FastDiv fd_members, fd_splits, fd_hblocks, fd_kv_heads;  // block-index divisors (indices < 2^31)
+  // fused append (k/v given): positions >= s_b are read from k/v, and each new
+  // token is stored into the cache by the one workgroup that owns it
+  const char* k_new;
+  const char* v_new;
+  int64_t k_sb, k_st, k_sh;
+  int64_t v_sb, v_st, v_sh;
+  int32_t* err;
+  int32_t fused;
 };
 
 template <typename TC> struct mfma_t;
@@ -120,22 +136,25 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int lr = lane % 16;
 
   // ---- block -> (group = (b, kv head, head block), q tile, split); a group's blocks share an XCD ----
-  const int64_t pb = blockIdx.x;
-  const int64_t pr = pb / kXcdsC;
-  const int members = p.n_qtiles * p.num_splits;
-  const int member = static_cast<int>(pr % members);
-  const int qt = member / p.num_splits;
-  const int split = member % p.num_splits;
-  const int64_t group = (pr / members) * kXcdsC + pb % kXcdsC;
+  const uint32_t pb = blockIdx.x;
+  uint32_t member, rem;
+  const uint32_t gq = fdivmod(pb / kXcdsC, p.fd_members, member);
+  const int qt = static_cast<int>(fdivmod(member, p.fd_splits, rem));
+  const int split = static_cast<int>(rem);
+  const uint32_t group = gq * kXcdsC + pb % kXcdsC;
   if (group >= p.n_groups) return;
-  int64_t gtmp = group;
-  const int hb = static_cast<int>(gtmp % p.n_hblocks); gtmp /= p.n_hblocks;
-  const int hk = static_cast<int>(gtmp % p.n_kv_heads);
-  const int64_t b = gtmp / p.n_kv_heads;
+  uint32_t gtmp = fdivmod(group, p.fd_hblocks, rem);
+  const int hb = static_cast<int>(rem);
+  const int64_t b = fdivmod(gtmp, p.fd_kv_heads, rem);
+  const int hk = static_cast<int>(rem);
 
   const int s = p.seqlens[b];
   const int q0 = qt * QB;
   const int q_end = min(q0 + QB, p.t_new);
+  if (p.fused && p.err != nullptr && qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0 &&
+      (s < 0 || s > p.t_max - p.t_new)) {
+    atomicOr(p.err, NC_DEVERR_OVERFLOW);  // a new token falls outside [0, t_max): not stored
+  }
 
   // this lane's query row
   const int row = wave * 16 + lr;
@@ -172,10 +191,19 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc_o[db] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-  const char* kbase = p.kc + (b * p.kc_sb + hk * p.kc_sh) * elem<TC>::kBytes;
-  const char* vbase = p.vc + (b * p.vc_sb + hk * p.vc_sh) * elem<TC>::kBytes;
-  const int64_t kst = p.kc_st * elem<TC>::kBytes;
-  const int64_t vst = p.vc_st * elem<TC>::kBytes;
+  constexpr int EB = elem<TC>::kBytes;
+  const char* kbase = p.kc + (b * p.kc_sb + hk * p.kc_sh) * EB;
+  const char* vbase = p.vc + (b * p.vc_sb + hk * p.vc_sh) * EB;
+  const int64_t kst = p.kc_st * EB;
+  const int64_t vst = p.vc_st * EB;
+  // new tokens: position j >= s is token j - s of k/v; this workgroup stores the
+  // ones of its own queries, [s + q0, s + q_end), once per kv head (hb == 0)
+  const int new_lo = p.fused ? s : INT32_MAX;
+  const int own_lo = (p.fused && hb == 0) ? s + q0 : INT32_MAX;
+  const char* knew = p.k_new + (b * p.k_sb + hk * p.k_sh) * EB;
+  const char* vnew = p.v_new + (b * p.v_sb + hk * p.v_sh) * EB;
+  const int64_t knst = p.k_st * EB;
+  const int64_t vnst = p.v_st * EB;
 
   // ---- key tiles: registers hold the next tile while the current one is consumed from LDS ----
   uint4 kreg[PER_THREAD], vreg[PER_THREAD];
@@ -186,8 +214,11 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
       const int j = kt0 + c / (D / 8);
       const int dc = c % (D / 8);
       if (j < hi) {
-        kreg[u] = *reinterpret_cast<const uint4*>(kbase + j * kst + dc * 16);
-        vreg[u] = *reinterpret_cast<const uint4*>(vbase + j * vst + dc * 16);
+        const bool from_new = j >= new_lo;
+        const char* kp = from_new ? knew + (j - s) * knst : kbase + j * kst;
+        const char* vp = from_new ? vnew + (j - s) * vnst : vbase + j * vst;
+        kreg[u] = *reinterpret_cast<const uint4*>(kp + dc * 16);
+        vreg[u] = *reinterpret_cast<const uint4*>(vp + dc * 16);
       } else {
         kreg[u] = make_uint4(0, 0, 0, 0);
         vreg[u] = make_uint4(0, 0, 0, 0);
@@ -204,6 +235,11 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
       const int dc = c % (D / 8);
       *reinterpret_cast<uint4*>(ks + key * KROW + dc * 16) = kreg[u];
       *reinterpret_cast<uint4*>(vs + key * VROW + dc * 16) = vreg[u];
+      const int j = kt0 + key;
+      if (j >= own_lo && j < hi) {
+        *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + j * kst + dc * 16) = kreg[u];
+        *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + j * vst + dc * 16) = vreg[u];
+      }
     }
     __syncthreads();
     if (kt0 + kBN < hi) load_regs(kt0 + kBN);
@@ -349,6 +385,16 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.keys_per_split = plan.chunk_keys_per_split;
   p.part_ml = s.part_ml;
   p.part_o = s.part_o;
+  p.fd_members = make_fastdiv(static_cast<uint32_t>(p.n_qtiles * p.num_splits));
+  p.fd_splits = make_fastdiv(static_cast<uint32_t>(p.num_splits));
+  p.fd_hblocks = make_fastdiv(static_cast<uint32_t>(p.n_hblocks));
+  p.fd_kv_heads = make_fastdiv(static_cast<uint32_t>(p.n_kv_heads));
+  p.fused = a.k != nullptr ? 1 : 0;
+  p.k_new = static_cast<const char*>(a.k);
+  p.v_new = static_cast<const char*>(a.v);
+  p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
+  p.v_sb = a.v_stride_b; p.v_st = a.v_stride_t; p.v_sh = a.v_stride_h;
+  p.err = a.error_flag;
   if (a.cache_dtype == NC_DTYPE_BF16) {
     return a.head_dim == 64 ? launch_c<bf16, 64>(p, plan.head_block, stream)
                             : launch_c<bf16, 128>(p, plan.head_block, stream);

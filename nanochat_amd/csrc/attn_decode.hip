@@ -100,6 +100,8 @@ struct DecodeParams {
   int32_t num_splits, keys_per_split;
   int32_t fused;
   int32_t merge_qb;  // split merge: 0 = decode splits (per query); > 0 = chunk splits (per QB-query tile)
+  // divisors of the block-index decompositions (every index is < 2^31: the plan caps the grid)
+  FastDiv fd_hblocks, fd_kv_heads, fd_t_new, fd_splits, fd_kps, fd_qb;
 };
 
 template <typename TC> struct dot_packed;
@@ -168,7 +170,11 @@ __device__ __forceinline__ KeyRange key_range(const DecodeParams& p, int64_t b, 
 #else
   r.kps = p.keys_per_split;
 #endif
+#if NC_DECODE_EVEN_SPLITS
   r.nsplit = r.n > 0 ? (r.n + r.kps - 1) / r.kps : 1;
+#else
+  r.nsplit = r.n > 0 ? static_cast<int>(fdiv(static_cast<uint32_t>(r.n + r.kps - 1), p.fd_kps)) : 1;
+#endif
   return r;
 }
 
@@ -178,14 +184,15 @@ struct GroupIdx {
   int t, hk, hb;
 };
 
-__device__ __forceinline__ GroupIdx group_index(const DecodeParams& p, int64_t group) {
+__device__ __forceinline__ GroupIdx group_index(const DecodeParams& p, uint32_t group) {
   GroupIdx r;
-  r.hb = static_cast<int>(group % p.n_hblocks);
-  group /= p.n_hblocks;
-  r.hk = static_cast<int>(group % p.n_kv_heads);
-  group /= p.n_kv_heads;
-  r.t = static_cast<int>(group % p.t_new);
-  r.b = group / p.t_new;
+  uint32_t rem;
+  group = fdivmod(group, p.fd_hblocks, rem);
+  r.hb = static_cast<int>(rem);
+  group = fdivmod(group, p.fd_kv_heads, rem);
+  r.hk = static_cast<int>(rem);
+  r.b = fdivmod(group, p.fd_t_new, rem);
+  r.t = static_cast<int>(rem);
   return r;
 }
 
@@ -207,7 +214,7 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
   if (p.merge_qb == 0) {
     nsplit = key_range(p, gi.b, gi.t).nsplit;
   } else {
-    const int q0 = gi.t / p.merge_qb * p.merge_qb;
+    const int q0 = static_cast<int>(fdiv(static_cast<uint32_t>(gi.t), p.fd_qb)) * p.merge_qb;
     nsplit = chunk_span(p.seqlens[gi.b], q0, min(q0 + p.merge_qb, p.t_new), p.t_max, p.window,
                         p.keys_per_split).nsplit;
   }
@@ -287,14 +294,16 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
 
   // ---- block -> (group, split) ----
 #if NC_DECODE_XCD_MAP
-  const int64_t pb = blockIdx.x;
-  const int64_t pr = pb / kXcds;
-  const int split = static_cast<int>(pr % p.num_splits);
-  const int64_t group = (pr / p.num_splits) * kXcds + pb % kXcds;
+  const uint32_t pb = blockIdx.x;
+  uint32_t split_u;
+  const uint32_t gq = fdivmod(pb / kXcds, p.fd_splits, split_u);
+  const int split = static_cast<int>(split_u);
+  const uint32_t group = gq * kXcds + pb % kXcds;
   if (group >= p.n_groups) return;
 #else
-  const int split = static_cast<int>(blockIdx.x % p.num_splits);
-  const int64_t group = blockIdx.x / p.num_splits;
+  uint32_t split_u;
+  const uint32_t group = fdivmod(blockIdx.x, p.fd_splits, split_u);
+  const int split = static_cast<int>(split_u);
 #endif
   const GroupIdx gi = group_index(p, group);
   const int64_t b = gi.b;
@@ -572,6 +581,15 @@ int64_t decode_grid(int64_t n_groups, int num_splits) {
 
 namespace {
 
+void set_divisors(DecodeParams& p) {
+  p.fd_hblocks = make_fastdiv(static_cast<uint32_t>(p.n_hblocks));
+  p.fd_kv_heads = make_fastdiv(static_cast<uint32_t>(p.n_kv_heads));
+  p.fd_t_new = make_fastdiv(static_cast<uint32_t>(p.t_new));
+  p.fd_splits = make_fastdiv(static_cast<uint32_t>(p.num_splits));
+  p.fd_kps = make_fastdiv(static_cast<uint32_t>(p.keys_per_split));
+  p.fd_qb = make_fastdiv(static_cast<uint32_t>(p.merge_qb > 0 ? p.merge_qb : 1));
+}
+
 DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, bool fused_append) {
   DecodeParams p;
   p.q = a.q; p.out = a.out;
@@ -599,6 +617,7 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.keys_per_split = plan.keys_per_split;
   p.fused = fused_append ? 1 : 0;
   p.merge_qb = 0;
+  set_divisors(p);
   return p;
 }
 
@@ -623,6 +642,7 @@ hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const
   p.num_splits = plan.chunk_splits;
   p.keys_per_split = plan.chunk_keys_per_split;
   p.merge_qb = chunk_rows_per_wg() / plan.head_block;
+  set_divisors(p);
   switch (a.head_dim) {
     case 32: return launch_merge_d<32>(p, plan.head_block, stream);
     case 64: return launch_merge_d<64>(p, plan.head_block, stream);

@@ -88,6 +88,9 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
     }
     plan->chunk_keys_per_split = static_cast<int>(ckps);
     plan->chunk_splits = static_cast<int>(cns);
+    // the chunk grid (block indices are decomposed in 32-bit arithmetic)
+    const int64_t cgroups = (a.batch * a.n_kv_heads * plan->n_hblocks + 7) / 8 * 8;
+    if (cgroups * ((a.t_new + qb - 1) / qb) * cns > INT32_MAX) return NC_ERR_BAD_SHAPE;
   }
   const int64_t merge_splits = plan->use_chunk ? plan->chunk_splits : ns;
   if (merge_splits > 1) {
@@ -213,8 +216,8 @@ int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
 
   bool fused = false;
   if (a.k != nullptr) {
-    if (a.t_new == 1) {
-      fused = true;
+    if (a.t_new == 1 || plan.use_chunk) {
+      fused = true;  // the decode / chunk kernel appends the new tokens itself
     } else {
       nc_append_args ap;
       ap.k_cache = a.k_cache; ap.v_cache = a.v_cache; ap.k = a.k; ap.v = a.v;

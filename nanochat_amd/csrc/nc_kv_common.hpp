@@ -163,6 +163,37 @@ __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Division of integers in [0, 2^31) by a divisor fixed for the whole launch,
+// as a multiply-high and a shift (Granlund & Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994, sec. 4: with
+// l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1, n / d =
+// (mulhi(m, n) + n) >> l; the sum cannot overflow for n < 2^31).  The
+// block-index decompositions of the kernels use it instead of the 32/64-bit
+// division sequences the compiler would emit for runtime divisors.
+struct FastDiv {
+  uint32_t d, m, l;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  f.l = 0;
+  while ((uint64_t(1) << f.l) < d) ++f.l;
+  f.m = static_cast<uint32_t>(((uint64_t(1) << 32) * ((uint64_t(1) << f.l) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.l;
+}
+
+// q = n / d and r = n % d.
+__device__ __forceinline__ uint32_t fdivmod(uint32_t n, const FastDiv& f, uint32_t& r) {
+  const uint32_t q = fdiv(n, f);
+  r = n - q * f.d;
+  return q;
+}
+
 // Key span [lo, hi) of the chunk-kernel workgroup that owns queries
 // [q0, q_end) of a row whose cache held s tokens, and its split count (>= 1;
 // an empty span is one split).  The chunk kernel and the split merge both use

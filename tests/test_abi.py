@@ -182,3 +182,32 @@ def test_prefill_on_cpu_fails_loudly():
     dst = KVCache(2, 2, 8, 8, 1, "cpu", torch.float32)
     with pytest.raises(RuntimeError, match="GPU"):
         dst.prefill(src)
+
+
+def test_invariant_divisor_method_is_exact():
+    """The kernels split block indices with q = (mulhi(m, n) + n) >> l, m = floor(2^32 (2^l - d) / d) + 1,
+    l = ceil(log2 d) (Granlund & Montgomery 1994, sec. 4), for n < 2^31.  Check the identity against
+    integer division: every n < 4096 for d <= 300, and the extremes of the range for larger d."""
+    def make(d):
+        l = (d - 1).bit_length()
+        return ((1 << 32) * ((1 << l) - d)) // d + 1, l
+
+    def fdiv(n, m, l):
+        return (((m * n) >> 32) + n) >> l
+
+    for d in range(1, 301):
+        m, l = make(d)
+        assert m < (1 << 32)
+        for n in range(4096):
+            assert fdiv(n, m, l) == n // d, (n, d)
+    g = torch.Generator().manual_seed(0)
+    big = [2**31 - 1, 2**31 - 2, 2**30, 2**30 + 1, 3 * 2**29, 65537, 1 << 20, (1 << 20) + 1]
+    big += torch.randint(1, 2**31 - 1, (200,), generator=g).tolist()
+    for d in big:
+        m, l = make(d)
+        assert m < (1 << 32)
+        ns = [0, 1, d - 1, d, d + 1, 2**31 - 1, (2**31 - 1) // d * d, (2**31 - 1) // d * d - 1]
+        ns += torch.randint(0, 2**31, (64,), generator=g).tolist()
+        for n in ns:
+            if 0 <= n < 2**31:
+                assert fdiv(n, m, l) == n // d, (n, d)

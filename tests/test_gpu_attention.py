@@ -240,3 +240,51 @@ def test_mfma_chunk_split_sizes(kps, window):
     """Split-K of the chunk kernel: q tiles of one call have different split counts (ragged rows, causal
     spans, windows); one-split tiles write directly, the others go through the merge."""
     _check(220, 3, 100, 8, 2, 128, 1200, [0, 37, 1000], window, kps=kps)
+
+
+def test_mfma_chunk_overflow_stores_in_range_tokens_and_flags():
+    """Chunk append past t_max (the reference raises at flash_attention.py:161): the kernel stores the
+    tokens below t_max, skips the rest, sets the overflow flag, and leaves other rows' bytes alone."""
+    dev = torch.device(DEV, torch.cuda.current_device())
+    _ext.read_and_clear_device_errors(dev)
+    T_new, T_max = 20, 40
+    q, k, v, kc, vc, sl = _inputs(98, 2, T_new, 4, 2, 64, T_max, [5, 30], torch.bfloat16, torch.bfloat16)
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    out = flash_attn.flash_attn_with_kvcache(q.to(DEV), kc_d, vc_d, k=k.to(DEV), v=v.to(DEV),
+                                             cache_seqlens=sl.to(DEV), causal=True)
+    assert _ext.read_and_clear_device_errors(dev) & _ext.NC_DEVERR_OVERFLOW
+    assert torch.isfinite(out.float()).all()
+    kc_exp, vc_exp = kc.clone(), vc.clone()
+    kc_exp[0, 5:25] = k[0]
+    vc_exp[0, 5:25] = v[0]
+    kc_exp[1, 30:40] = k[1, :10]
+    vc_exp[1, 30:40] = v[1, :10]
+    assert torch.equal(bits(kc_d), bits(kc_exp))
+    assert torch.equal(bits(vc_d), bits(vc_exp))
+    # the in-range row is exact attention
+    ref = orc.flash_attn_with_kvcache(q[:1], kc[:1].clone(), vc[:1].clone(), k=k[:1], v=v[:1],
+                                      cache_seqlens=sl[:1], causal=True, compute_dtype=torch.float32)
+    assert max_rel_err(out[:1], ref.float()) <= 2e-2
+
+
+def test_mfma_chunk_reads_strided_new_kv():
+    """k/v as views of a fused (B, T, 2, H_kv, D) projection output: the chunk kernel takes the new
+    tokens straight from the strided k/v and stores them into the cache."""
+    g = gen(97)
+    B, T_new, H, H_kv, D, T_max = 2, 48, 8, 4, 128, 300
+    seqlens = [0, 211]
+    q = randn((B, T_new, H, D), g, torch.bfloat16)
+    kv = randn((B, T_new, 2, H_kv, D), g, torch.bfloat16)
+    kc = torch.zeros(B, T_max, H_kv, D, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kc[1, :211] = randn((211, H_kv, D), g, torch.bfloat16)
+    vc[1, :211] = randn((211, H_kv, D), g, torch.bfloat16)
+    sl = torch.tensor(seqlens, dtype=torch.int32)
+    kv_d = kv.to(DEV)
+    kc_d, vc_d = kc.to(DEV), vc.to(DEV)
+    out = flash_attn.flash_attn_with_kvcache(q.to(DEV), kc_d, vc_d, k=kv_d[:, :, 0], v=kv_d[:, :, 1],
+                                             cache_seqlens=sl.to(DEV), causal=True, window_size=(100, 0))
+    ref = orc.flash_attn_with_kvcache(q, kc, vc, k=kv[:, :, 0], v=kv[:, :, 1], cache_seqlens=sl, causal=True,
+                                      window_size=(100, 0), compute_dtype=torch.float32)
+    assert max_rel_err(out, ref.float()) <= 2e-2
+    assert torch.equal(bits(kc_d), bits(kc)) and torch.equal(bits(vc_d), bits(vc))
