@@ -196,19 +196,39 @@ __device__ __forceinline__ GroupIdx group_index(const DecodeParams& p, uint32_t 
   return r;
 }
 
-constexpr int kMergeChunk = 16;
+// Threads of a merge block: one per VE outputs of the group's GB heads.
+__host__ __device__ constexpr int merge_threads(int d, int gb, int ve) {
+  return (gb * d / ve + kWave - 1) / kWave * kWave < 256 ? (gb * d / ve + kWave - 1) / kWave * kWave : 256;
+}
+
+template <int VE> struct MergeVec;
+template <> struct MergeVec<1> {
+  typedef float T;
+  __device__ __forceinline__ static void get(const T& v, float (&o)[1]) { o[0] = v; }
+};
+template <> struct MergeVec<4> {
+  typedef float4 T;
+  __device__ __forceinline__ static void get(const T& v, float (&o)[4]) {
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  }
+};
 
 // Second pass: block g combines the split partials of group g's GB heads.
 // The block recomputes how many splits its query's producer used (decode:
 // the query's key range; chunk: its workgroup's span) and reads exactly those
 // slots; a query with one split was written directly by its producer.  Each
-// thread owns one output element and folds the slots in chunks of 16 with
-// all loads of a chunk in flight together, so up to 16 splits cost one
-// memory round trip; the (m, l) reads are uniform per head (one transaction
-// per wave).  Slots with l == 0 (every key of the split masked for this
-// query) contribute nothing.
-template <int D, int GB>
+// thread owns VE consecutive output elements of one head and folds the slots
+// in chunks of CH with every load of a chunk in flight together ((m, l) reads
+// are uniform per head), so up to CH splits cost one memory round trip.  The
+// number of dependent round trips, not the bytes, sets this kernel's time;
+// two shapes are instantiated: <CH 16, VE 1> (few VGPRs, high occupancy: many
+// merge blocks, few splits) and <CH 32, VE 4> (decode with more than 16
+// splits: one or two round trips for up to 64 splits).  Slots with l == 0
+// (every key of the split masked for this query) contribute nothing.
+template <int D, int GB, int CH, int VE>
 __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p) {
+  typedef typename MergeVec<VE>::T VT;
+  constexpr int TPH = D / VE;  // threads per head
   const GroupIdx gi = group_index(p, blockIdx.x);
   int nsplit;
   if (p.merge_qb == 0) {
@@ -218,54 +238,75 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
     nsplit = chunk_span(p.seqlens[gi.b], q0, min(q0 + p.merge_qb, p.t_new), p.t_max, p.window,
                         p.keys_per_split).nsplit;
   }
-  // Decode splits with at most 16 slots: load every allocated slot without
+  // Decode splits with at most CH slots: load every allocated slot without
   // waiting for cache_seqlens (one memory round trip instead of two); slots
   // past the query's split count hold stale data and are masked out below.
-  const bool eager = p.merge_qb == 0 && p.num_splits <= kMergeChunk;
+  const bool eager = p.merge_qb == 0 && p.num_splits <= CH;
   if (!eager && nsplit <= 1) return;
   const int lim = eager ? p.num_splits : nsplit;
   const int64_t pair0 = (gi.b * p.t_new + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;
-  for (int idx = threadIdx.x; idx < GB * D; idx += blockDim.x) {
-    const int g = idx / D, d = idx % D;
+  for (int e = threadIdx.x; e < GB * TPH; e += blockDim.x) {
+    const int g = e / TPH, d0 = (e % TPH) * VE;
     const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
-    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d;
-    float M = kNegBig, L = 0.0f, O = 0.0f;
-    for (int sp0 = 0; sp0 < lim; sp0 += kMergeChunk) {
-      float ms[kMergeChunk], ls[kMergeChunk], os[kMergeChunk];
+    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d0;
+    float M = kNegBig, L = 0.0f, O[VE];
 #pragma unroll
-      for (int u = 0; u < kMergeChunk; ++u) {
+    for (int v = 0; v < VE; ++v) O[v] = 0.0f;
+    for (int sp0 = 0; sp0 < lim; sp0 += CH) {
+      float ms[CH], ls[CH];
+      VT os[CH];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
         const int sp = sp0 + u;
         if (sp < lim) {
           const float2 v = *reinterpret_cast<const float2*>(ml + 2 * sp);
           ms[u] = v.x;
           ls[u] = v.y;
-          os[u] = po[static_cast<int64_t>(sp) * D];
+          os[u] = *reinterpret_cast<const VT*>(po + static_cast<int64_t>(sp) * D);
         } else {
           ms[u] = kNegBig;
           ls[u] = 0.0f;
-          os[u] = 0.0f;
+          os[u] = VT{};
         }
       }
 #pragma unroll
-      for (int u = 0; u < kMergeChunk; ++u) {
+      for (int u = 0; u < CH; ++u) {
         if (sp0 + u >= nsplit) ls[u] = 0.0f;  // slot not written by this call
       }
       float mx = M;
 #pragma unroll
-      for (int u = 0; u < kMergeChunk; ++u) mx = ls[u] > 0.0f ? fmaxf(mx, ms[u]) : mx;
+      for (int u = 0; u < CH; ++u) mx = ls[u] > 0.0f ? fmaxf(mx, ms[u]) : mx;
       const float a = fast_exp2(M - mx);
       L *= a;
-      O *= a;
 #pragma unroll
-      for (int u = 0; u < kMergeChunk; ++u) {
-        const float w = ls[u] > 0.0f ? fast_exp2(ms[u] - mx) : 0.0f;
+      for (int v = 0; v < VE; ++v) O[v] *= a;
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const bool live = ls[u] > 0.0f;
+        const float w = live ? fast_exp2(ms[u] - mx) : 0.0f;
         L = __builtin_fmaf(ls[u], w, L);
-        O = ls[u] > 0.0f ? __builtin_fmaf(os[u], w, O) : O;
+        float ov[VE];
+        MergeVec<VE>::get(os[u], ov);
+#pragma unroll
+        for (int v = 0; v < VE; ++v) O[v] = live ? __builtin_fmaf(ov[v], w, O[v]) : O[v];
       }
       M = mx;
     }
     if (nsplit <= 1) return;  // the producer wrote this query's output
-    store_any(p.out, (pair0 + g) * D + d, p.q_dtype, L > 0.0f ? O / L : 0.0f);
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const int64_t o0 = (pair0 + g) * D + d0;
+#pragma unroll
+    for (int v = 0; v < VE; ++v) store_any(p.out, o0 + v, p.q_dtype, O[v] * inv);
+  }
+}
+
+template <int D, int GB>
+void launch_merge_g(const DecodeParams& p, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.n_groups));
+  if (p.merge_qb == 0 && p.num_splits > 16) {
+    hipLaunchKernelGGL((merge_splits_kernel<D, GB, 32, 4>), grid, dim3(merge_threads(D, GB, 4)), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((merge_splits_kernel<D, GB, 16, 1>), grid, dim3(merge_threads(D, GB, 1)), 0, stream, p);
   }
 }
 
@@ -528,15 +569,12 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
   }
 }
 
+
 template <typename TC, bool QPK, int D, int GB>
 hipError_t launch_g(const DecodeParams& p, int64_t n_wg, hipStream_t stream) {
   hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB>), dim3(static_cast<unsigned>(n_wg)),
                      dim3(kWavesPerWG * kWave), 0, stream, p);
-  if (p.num_splits > 1) {
-    const int threads = std::min(256, (GB * D + kWave - 1) / kWave * kWave);
-    hipLaunchKernelGGL((merge_splits_kernel<D, GB>), dim3(static_cast<unsigned>(p.n_groups)), dim3(threads), 0,
-                       stream, p);
-  }
+  if (p.num_splits > 1) launch_merge_g<D, GB>(p, stream);
   return hipGetLastError();
 }
 
@@ -623,13 +661,11 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
 
 template <int D>
 hipError_t launch_merge_d(const DecodeParams& p, int gb, hipStream_t stream) {
-  const int threads = std::min(256, (gb * D + kWave - 1) / kWave * kWave);
-  const dim3 grid(static_cast<unsigned>(p.n_groups)), block(threads);
   switch (gb) {
-    case 8: hipLaunchKernelGGL((merge_splits_kernel<D, 8>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((merge_splits_kernel<D, 4>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((merge_splits_kernel<D, 2>), grid, block, 0, stream, p); break;
-    default: hipLaunchKernelGGL((merge_splits_kernel<D, 1>), grid, block, 0, stream, p); break;
+    case 8: launch_merge_g<D, 8>(p, stream); break;
+    case 4: launch_merge_g<D, 4>(p, stream); break;
+    case 2: launch_merge_g<D, 2>(p, stream); break;
+    default: launch_merge_g<D, 1>(p, stream); break;
   }
   return hipGetLastError();
 }

@@ -288,3 +288,10 @@ def test_mfma_chunk_reads_strided_new_kv():
                                       window_size=(100, 0), compute_dtype=torch.float32)
     assert max_rel_err(out, ref.float()) <= 2e-2
     assert torch.equal(bits(kc_d), bits(kc)) and torch.equal(bits(vc_d), bits(vc))
+
+
+@pytest.mark.parametrize("H,H_kv,kps", [(16, 4, 128), (8, 1, 64), (6, 6, 128)])
+def test_decode_merge_beyond_16_splits(H, H_kv, kps):
+    """Rows of 40+ splits take the 32-slot merge (float4 per thread), short rows in the same call
+    write directly or merge a few slots."""
+    _check(230 + H, 3, 1, H, H_kv, 128, 5200, [5000, 70, 2100], -1, kps=kps)
