@@ -62,6 +62,9 @@
 #ifndef NC_DECODE_EVEN_SPLITS
 #define NC_DECODE_EVEN_SPLITS 0 // 1: every split of a row gets ceil(n / num_splits) keys (no empty splits)
 #endif
+#ifndef NC_DECODE_PV_DOT2
+#define NC_DECODE_PV_DOT2 1     // 1: P.V with v_dot2 on key pairs (packed caches)
+#endif
 #ifndef NC_DECODE_KEY_BYTES
 #define NC_DECODE_KEY_BYTES 65536  // default split: this many K bytes per unit (and as many V)
 #endif
@@ -110,11 +113,20 @@ template <> struct dot_packed<bf16> {
   __device__ __forceinline__ static float run(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
   }
+  // two fp32 values rounded to nearest-even and packed (x0 low)
+  __device__ __forceinline__ static uint32_t pack(float x0, float x1) {
+    const v2 v = {static_cast<__bf16>(x0), static_cast<__bf16>(x1)};
+    return __builtin_bit_cast(uint32_t, v);
+  }
 };
 template <> struct dot_packed<f16> {
   typedef _Float16 v2 __attribute__((ext_vector_type(2)));
   __device__ __forceinline__ static float run(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+  __device__ __forceinline__ static uint32_t pack(float x0, float x1) {
+    const v2 v = {static_cast<_Float16>(x0), static_cast<_Float16>(x1)};
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 
@@ -431,16 +443,42 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o[g][e] *= alpha;
     }
+    if constexpr (QPK && NC_DECODE_PV_DOT2 && NI % 2 == 0) {
+      // P.V on key pairs with v_dot2: P rounded to the cache dtype (as in
+      // flash-attention's second matmul), the two keys' elements of one dim
+      // paired by v_perm; the sum l stays in fp32.
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
-      float vf[VEC];
-      widen<TC>::run(vv[i], vf);
+      for (int i = 0; i < NI; i += 2) {
+        const uint32_t a[4] = {vv[i].x, vv[i].y, vv[i].z, vv[i].w};
+        const uint32_t c[4] = {vv[i + 1].x, vv[i + 1].y, vv[i + 1].z, vv[i + 1].w};
+        uint32_t pairs[VEC];
 #pragma unroll
-      for (int g = 0; g < GB; ++g) {
-        const float pr = fast_exp2(sc[g][i] - m[g]);
-        l[g] += pr;
+        for (int w = 0; w < 4; ++w) {
+          pairs[2 * w] = __builtin_amdgcn_perm(c[w], a[w], 0x05040100u);      // element 2w of keys i, i+1
+          pairs[2 * w + 1] = __builtin_amdgcn_perm(c[w], a[w], 0x07060302u);  // element 2w+1
+        }
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) o[g][e] = __builtin_fmaf(pr, vf[e], o[g][e]);
+        for (int g = 0; g < GB; ++g) {
+          const float p0 = fast_exp2(sc[g][i] - m[g]);
+          const float p1 = fast_exp2(sc[g][i + 1] - m[g]);
+          l[g] += p0 + p1;
+          const uint32_t pp = dot_packed<TC>::pack(p0, p1);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[g][e] = dot_packed<TC>::run(pp, pairs[e], o[g][e]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        float vf[VEC];
+        widen<TC>::run(vv[i], vf);
+#pragma unroll
+        for (int g = 0; g < GB; ++g) {
+          const float pr = fast_exp2(sc[g][i] - m[g]);
+          l[g] += pr;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) o[g][e] = __builtin_fmaf(pr, vf[e], o[g][e]);
+        }
       }
     }
   };
