@@ -325,6 +325,61 @@ def run_c3(dev, stream, steps, kps=0, ckps=0):
             "decode_GB_per_s": round(dec_bytes / (ms_dec * 1e-3) / 1e9, 1)}
 
 
+def run_e2e(dev, stream, steps, kps=0, ckps=0):
+    """d20 model decode step (random-init weights, bf16, SSSL windows at sequence_len 2048): B=32 rows at
+    position 1280, one token per row per step.  Three timings of GPT.forward with the cache:
+    the reference's op-by-op QK prologue (eager; it needs get_pos(), a host sync), the fused prologue
+    (eager), and the fused prologue with one decode step captured in a HIP graph (possible because the
+    fused path has no host sync)."""
+    from nanochat_amd.engine import KVCache
+    from nanochat_amd.gpt import GPTConfig, build_model
+    cfg = GPTConfig(sequence_len=2048, vocab_size=32768, n_layer=20, n_head=10, n_kv_head=10, n_embd=1280)
+    B, P = 32, 1280
+    with torch.cuda.stream(stream):
+        model = build_model(cfg, dev, compute_dtype=torch.bfloat16, seed=0)
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        kv = KVCache(B, 10, P + 3 * steps + 16, 128, 20, dev, torch.bfloat16)
+        kv.k_cache[:, :, :P].normal_(generator=g)
+        kv.v_cache[:, :, :P].normal_(generator=g)
+        ids = torch.randint(0, 32768, (B, 1), generator=g, device=dev)
+
+    def timed(fn, n):
+        with torch.cuda.stream(stream):
+            fn()
+            stream.synchronize()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            for _ in range(n):
+                fn()
+            ev1.record(stream)
+            stream.synchronize()
+            return ev0.elapsed_time(ev1) / n
+
+    def step():
+        with torch.inference_mode():
+            model.forward(ids, kv_cache=kv)
+
+    res = {}
+    for name, fused in (("op_by_op_eager", False), ("fused_eager", True)):
+        model.fused_qk_prologue = fused
+        kv.cache_seqlens.fill_(P)
+        res[name] = timed(step, steps)
+    model.fused_qk_prologue = True
+    kv.cache_seqlens.fill_(P)
+    with torch.cuda.stream(stream):
+        step()  # warm the workspace on this stream
+        stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.inference_mode(), torch.cuda.graph(graph, stream=stream):
+        model.forward(ids, kv_cache=kv)
+    kv.cache_seqlens.fill_(P)
+    res["fused_graph"] = timed(graph.replay, steps)
+    return {"config": "e2e", "workload": f"d20 GPT decode step (random init, bf16, SSSL), B={B} at position {P}, "
+                                         f"{steps} steps", **{k + "_ms_per_step": round(v, 4) for k, v in res.items()},
+            "tokens_per_s_fused_graph": round(B / (res["fused_graph"] * 1e-3), 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -336,8 +391,11 @@ def main() -> int:
     ap.add_argument("--chunk-keys-per-split", type=int, default=0,
                     help="c3/c5 chunk-kernel split size (0 = library default)")
     ap.add_argument("--eager", action="store_true", help="also time the steps without a graph")
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5"],
-                    help="c2 (default) is the metric line; c3/c4/c5 print per-phase figures")
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "e2e"],
+                    help="c2 (default) is the metric line; c3/c4/c5 print per-phase figures; e2e times the d20 "
+                         "model's decode step")
+    ap.add_argument("--rope", action="store_true",
+                    help="c2 through flash_attn_with_kvcache_rope (QK prologue fused; same bytes + tables)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -350,8 +408,9 @@ def main() -> int:
         dev = torch.device("cuda", 0)
         torch.cuda.set_device(dev)
         stream = torch.cuda.Stream(device=dev)
-        runner = {"c3": run_c3, "c4": run_c4, "c5": run_c5}[args.config]
-        steps = {"c3": min(args.steps, 128), "c4": min(args.steps, 256), "c5": min(args.steps, 16)}[args.config]
+        runner = {"c3": run_c3, "c4": run_c4, "c5": run_c5, "e2e": run_e2e}[args.config]
+        steps = {"c3": min(args.steps, 128), "c4": min(args.steps, 256), "c5": min(args.steps, 16),
+                 "e2e": min(args.steps, 64)}[args.config]
         print(json.dumps(runner(dev, stream, steps, kps=args.keys_per_split, ckps=args.chunk_keys_per_split)),
               flush=True)
         return 0
@@ -385,11 +444,21 @@ def main() -> int:
         seqlens = s0.to(dev)
         s0_dev = s0.to(dev)
 
+        if args.rope:
+            from nanochat_amd.flash_attention import flash_attn_with_kvcache_rope
+            from nanochat_amd.gpt import rotary_tables
+            cos_t, sin_t = rotary_tables(10 * 2048, HEAD_DIM, device=dev, dtype=torch.bfloat16)
+
         def one_step(i):
             for layer in range(LAYERS):
-                flash_attn_with_kvcache(q_all[i, layer], k_cache[layer], v_cache[layer], k=k_all[i, layer],
-                                        v=v_all[i, layer], cache_seqlens=seqlens, causal=True,
-                                        window_size=(-1, 0), keys_per_split=args.keys_per_split)
+                if args.rope:
+                    flash_attn_with_kvcache_rope(q_all[i, layer], k_cache[layer], v_cache[layer], k_all[i, layer],
+                                                 v_all[i, layer], seqlens, cos_t, sin_t, causal=True,
+                                                 window_size=(-1, 0), keys_per_split=args.keys_per_split)
+                else:
+                    flash_attn_with_kvcache(q_all[i, layer], k_cache[layer], v_cache[layer], k=k_all[i, layer],
+                                            v=v_all[i, layer], cache_seqlens=seqlens, causal=True,
+                                            window_size=(-1, 0), keys_per_split=args.keys_per_split)
             seqlens.add_(1)
 
         # eager warmup (allocates the split-K workspace on this stream)

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NC_KV_ABI_VERSION 1
+#define NC_KV_ABI_VERSION 2
 
 /* Element types (the torch dtypes the reference path uses). */
 enum nc_dtype {
@@ -147,6 +147,42 @@ typedef struct nc_attn_args {
 size_t nc_attn_workspace_bytes(const nc_attn_args* args);
 
 int nc_attn_kvcache(const nc_attn_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * QK prologue fused into the call: nanochat/gpt.py:98-102 (rotary, QK RMS
+ * norm, x qk_scale), which the reference computes with separate torch ops
+ * before flash_attn_with_kvcache (gpt.py:112-118), applied here to the raw q
+ * and k projections with each row's position from cache_seqlens:
+ *   token t of row b uses table row r = cache_seqlens[b] + t;
+ *   y1 = x1 cos[r] + x2 sin[r],  y2 = -x1 sin[r] + x2 cos[r]
+ *        (x1, x2: dims [0, D/2) and [D/2, D); nanochat/gpt.py:57-63);
+ *   y  = qk_scale * y / sqrt(mean(y^2) + eps)            (gpt.py:42-43).
+ * q is transformed for the attention only (rounded to q's dtype); k is
+ * transformed, rounded to the cache dtype (RNE) and appended with v, which is
+ * appended unchanged.  Arithmetic is fp32 with one rounding at the end (the
+ * reference rounds after every op in its compute dtype).  The reference
+ * slices the tables at row 0's position (gpt.py:424-425); per-row positions
+ * equal that for uniform batches.  A table row at or past rot_len is read as
+ * row rot_len - 1 and sets NC_DEVERR_ROPE_RANGE (the reference asserts,
+ * gpt.py:420).  k and v are required.  T_new == 1 runs in the decode kernel
+ * itself; T_new > 1 runs a prologue kernel (q into the workspace, k/v into
+ * the cache) and then the attention of nc_attn_kvcache without append.
+ * ------------------------------------------------------------------------- */
+#define NC_DEVERR_ROPE_RANGE 2
+
+typedef struct nc_qk_prologue {
+  const void* cos;               /* (rot_len, head_dim / 2), contiguous, 16-byte aligned (gpt.py:268-283) */
+  const void* sin;
+  int64_t rot_len;
+  int32_t rot_dtype;             /* dtype of cos / sin */
+  float qk_scale;                /* nanochat: 1.2 */
+  float eps;                     /* rms_norm eps: torch.finfo(compute dtype).eps */
+} nc_qk_prologue;
+
+/* Bytes of workspace nc_attn_kvcache_rope needs (>= nc_attn_workspace_bytes). */
+size_t nc_attn_rope_workspace_bytes(const nc_attn_args* args);
+
+int nc_attn_kvcache_rope(const nc_attn_args* args, const nc_qk_prologue* prologue, void* stream);
 
 /* Name of an nc_status code (static string). */
 const char* nc_strerror(int status);

@@ -16,11 +16,12 @@ import torch
 # NANOCHAT_AMD_LIB points at another build of the same library (e.g. a tuning
 # variant); by default the in-tree build next to this file is loaded.
 LIB_PATH = Path(os.environ.get("NANOCHAT_AMD_LIB", Path(__file__).resolve().parent / "libnc_kv.so"))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 NC_DEVERR_OVERFLOW = 1
+NC_DEVERR_ROPE_RANGE = 2
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -73,6 +74,14 @@ class AttnArgs(ctypes.Structure):
     ]
 
 
+class QKPrologue(ctypes.Structure):
+    _fields_ = [
+        ("cos", _c_void_p), ("sin", _c_void_p),
+        ("rot_len", _i64), ("rot_dtype", _i32),
+        ("qk_scale", ctypes.c_float), ("eps", ctypes.c_float),
+    ]
+
+
 # Every function include/nc_kv.h declares, with its ctypes signature.
 EXPORTS = {
     "nc_abi_version": (ctypes.c_int, []),
@@ -82,6 +91,8 @@ EXPORTS = {
     "nc_kv_fanout": (ctypes.c_int, [ctypes.POINTER(FanoutArgs), _c_void_p]),
     "nc_attn_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
     "nc_attn_kvcache": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _c_void_p]),
+    "nc_attn_rope_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
+    "nc_attn_kvcache_rope": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.POINTER(QKPrologue), _c_void_p]),
 }
 
 _lib = None

@@ -56,9 +56,6 @@
 #ifndef NC_DECODE_NT_LOADS
 #define NC_DECODE_NT_LOADS 1    // 1: K/V loads carry the non-temporal hint (+12% measured)
 #endif
-#ifndef NC_DECODE_PIPELINE
-#define NC_DECODE_PIPELINE 0    // 1: the next tile's loads are issued before the current tile is consumed
-#endif
 #ifndef NC_DECODE_EVEN_SPLITS
 #define NC_DECODE_EVEN_SPLITS 0 // 1: every split of a row gets ceil(n / num_splits) keys (no empty splits)
 #endif
@@ -103,6 +100,11 @@ struct DecodeParams {
   int32_t num_splits, keys_per_split;
   int32_t fused;
   int32_t merge_qb;  // split merge: 0 = decode splits (per query); > 0 = chunk splits (per QB-query tile)
+  // fused QK prologue (rotary, RMS norm, scale) on q and the appended k; rope == 0: off
+  const void* rope_cos;
+  const void* rope_sin;
+  int32_t rope, rope_len, rope_dtype, rope_half;  // rope_half = head_dim / 2 (table row length)
+  float rope_scale, rope_eps;
   // divisors of the block-index decompositions (every index is < 2^31: the plan caps the grid)
   FastDiv fd_hblocks, fd_kv_heads, fd_t_new, fd_splits, fd_kps, fd_qb;
 };
@@ -379,18 +381,14 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
 
   const int h0 = hk * p.group + hb * GB;          // first q head of this unit
 
-  // ---- query fragments ----
-  QFrag<TC, QPK> qf[GB];
-#pragma unroll
-  for (int g = 0; g < GB; ++g) {
-    const int64_t qoff = b * p.q_sb + t * p.q_st + (h0 + g) * p.q_sh + col * VEC;
-    if constexpr (QPK) {
-      qf[g].w = *reinterpret_cast<const uint4*>(static_cast<const char*>(p.q) + qoff * EB);
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) qf[g].f[e] = load_any(p.q, qoff + e, p.q_dtype);
-    }
+  // table row of the fused QK prologue: the query's position, clamped into the table
+  const int rope_row = min(max(qpos, 0), p.rope_len - 1);
+  if (p.rope && (qpos < 0 || qpos >= p.rope_len) && split == 0 && hk == 0 && hb == 0 && tid == 0 &&
+      p.err != nullptr) {
+    atomicOr(p.err, NC_DEVERR_ROPE_RANGE);
   }
+
+  QFrag<TC, QPK> qf[GB];  // filled once the first tile's loads are in flight
 
   float m[GB], l[GB], o[GB][VEC];
 #pragma unroll
@@ -483,35 +481,70 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
     }
   };
   constexpr int STEP = NW * TILE;
-#if NC_DECODE_PIPELINE
-  {
-    // two register buffers; the loads of the next tile are in flight while this one is consumed
-    uint4 ka[NI], va[NI], kb2[NI], vb2[NI];
-    int base = k0 + wave * TILE;
-    if (base < kc_end) load_tile(base, ka, va);
-    while (base < kc_end) {
-      if (base + STEP < kc_end) load_tile(base + STEP, kb2, vb2);
-      consume_tile(base, ka, va);
-      base += STEP;
-      if (base >= kc_end) break;
-      if (base + STEP < kc_end) load_tile(base + STEP, ka, va);
-      consume_tile(base, kb2, vb2);
-      base += STEP;
+  // the first tile's loads go out before q is prepared (the QK prologue's
+  // table loads and shuffles then overlap them); afterwards each tile's loads
+  // are issued right after the previous one is consumed
+  uint4 kv[NI], vv[NI];
+  int base = k0 + wave * TILE;
+  if (base < kc_end) load_tile(base, kv, vv);
+  float rcos[VEC], rsin[VEC];  // this lane's table entries (fused QK prologue)
+  if (p.rope) {
+    const int64_t toff = static_cast<int64_t>(rope_row) * p.rope_half + (col % (LPK / 2)) * VEC;
+    load_table_vec<VEC>(p.rope_cos, toff, p.rope_dtype, rcos);
+    load_table_vec<VEC>(p.rope_sin, toff, p.rope_dtype, rsin);
+  }
+  // ---- query fragments (raw, or through the QK prologue and rounded to q's dtype), built while
+  // the first tile's K/V loads are in flight ----
+#pragma unroll
+  for (int g = 0; g < GB; ++g) {
+    const int64_t qoff = b * p.q_sb + t * p.q_st + (h0 + g) * p.q_sh + col * VEC;
+    if (p.rope) {
+      float xf[VEC];
+      if constexpr (QPK) {
+        widen<TC>::run(*reinterpret_cast<const uint4*>(static_cast<const char*>(p.q) + qoff * EB), xf);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) xf[e] = load_any(p.q, qoff + e, p.q_dtype);
+      }
+      qk_prologue_apply<LPK, VEC>(xf, col, rcos, rsin, p.rope_scale, p.rope_eps);
+      if constexpr (QPK) {
+        qf[g].w = pack_cache_vec<TC>(xf);  // q's dtype is the cache dtype on this path
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) qf[g].f[e] = round_to(xf[e], p.q_dtype);
+      }
+    } else if constexpr (QPK) {
+      qf[g].w = *reinterpret_cast<const uint4*>(static_cast<const char*>(p.q) + qoff * EB);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) qf[g].f[e] = load_any(p.q, qoff + e, p.q_dtype);
     }
   }
-#else
-  for (int base = k0 + wave * TILE; base < kc_end; base += STEP) {
-    uint4 kv[NI], vv[NI];
-    load_tile(base, kv, vv);
+
+  while (base < kc_end) {
     consume_tile(base, kv, vv);
+    base += STEP;
+    if (base < kc_end) load_tile(base, kv, vv);
   }
-#endif
 
   // ---- the appended token (fused path): read from k/v, store into the cache ----
   if (own_new && wave == NW - 1) {
     const int64_t koff = b * p.k_sb + hk * p.k_sh + col * VEC;
     const int64_t voff = b * p.v_sb + hk * p.v_sh + col * VEC;
-    const uint4 kn = load_as_cache_vec<TC>(p.k_new, koff, p.q_dtype);
+    uint4 kn;
+    if (p.rope) {
+      float xf[VEC];
+      if constexpr (QPK) {
+        widen<TC>::run(*reinterpret_cast<const uint4*>(static_cast<const char*>(p.k_new) + koff * EB), xf);
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) xf[e] = load_any(p.k_new, koff + e, p.q_dtype);
+      }
+      qk_prologue_apply<LPK, VEC>(xf, col, rcos, rsin, p.rope_scale, p.rope_eps);
+      kn = pack_cache_vec<TC>(xf);
+    } else {
+      kn = load_as_cache_vec<TC>(p.k_new, koff, p.q_dtype);
+    }
     const uint4 vn = load_as_cache_vec<TC>(p.v_new, voff, p.q_dtype);
     if (hb == 0 && row == 0) {
       *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + qpos * kst) = kn;
@@ -693,6 +726,13 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.keys_per_split = plan.keys_per_split;
   p.fused = fused_append ? 1 : 0;
   p.merge_qb = 0;
+  p.rope_cos = p.rope_sin = nullptr;
+  p.rope = 0;
+  p.rope_len = 1;
+  p.rope_half = static_cast<int32_t>(a.head_dim / 2);
+  p.rope_dtype = NC_DTYPE_F32;
+  p.rope_scale = 1.0f;
+  p.rope_eps = 0.0f;
   set_divisors(p);
   return p;
 }
@@ -726,8 +766,17 @@ hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const
 }
 
 hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
-                         bool fused_append, hipStream_t stream) {
-  const DecodeParams p = make_params(a, plan, s, fused_append);
+                         bool fused_append, const nc_qk_prologue* prologue, hipStream_t stream) {
+  DecodeParams p = make_params(a, plan, s, fused_append);
+  if (prologue != nullptr) {
+    p.rope = 1;
+    p.rope_cos = prologue->cos;
+    p.rope_sin = prologue->sin;
+    p.rope_len = static_cast<int32_t>(prologue->rot_len);
+    p.rope_dtype = prologue->rot_dtype;
+    p.rope_scale = prologue->qk_scale;
+    p.rope_eps = prologue->eps;
+  }
   const bool qpk = a.q_dtype == a.cache_dtype && a.cache_dtype != NC_DTYPE_F32;
   const int gb = plan.head_block;
   switch (a.cache_dtype) {

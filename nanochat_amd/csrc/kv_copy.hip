@@ -96,6 +96,96 @@ __global__ __launch_bounds__(256) void kv_fanout_kernel(const FanoutParams p) {
   }
 }
 
+// QK prologue for chunks (t_new > 1): one row of D elements per G = D/8 lanes,
+// rows enumerated (b, t, slot) with slots [0, H) the q heads, [H, H + H_kv)
+// the k heads and [H + H_kv, H + 2 H_kv) the v heads.  q and k go through
+// qk_prologue_lanes (rotary at table row s_b + t, RMS norm, scale); q is
+// written to q_out (contiguous, q's dtype), k and v are appended into the
+// cache at s_b + t (k rounded RNE to the cache dtype; v copied as copy_ does).
+struct RopeAppendParams {
+  const void* q;
+  void* q_out;
+  const void* k;
+  const void* v;
+  char* kc;
+  char* vc;
+  const int32_t* seqlens;
+  int32_t* err;
+  const void* cos;
+  const void* sin;
+  int64_t q_sb, q_st, q_sh, k_sb, k_st, k_sh, v_sb, v_st, v_sh;
+  int64_t kc_sb, kc_st, kc_sh, vc_sb, vc_st, vc_sh;
+  int64_t n_rows;                 // B * t_new * (H + 2 H_kv)
+  int32_t t_new, t_max, n_heads, n_kv_heads, q_dtype, cache_dtype, rot_len, rot_dtype;
+  float scale, eps;
+};
+
+// One element of a runtime-typed input into a runtime-typed tensor, as copy_
+// does (same dtype: the bits).
+__device__ __forceinline__ void copy_elem(void* dst, int64_t di, int out_dtype, const void* src, int64_t si,
+                                          int in_dtype) {
+  if (in_dtype == out_dtype) {
+    if (in_dtype == NC_DTYPE_F32) {
+      static_cast<uint32_t*>(dst)[di] = static_cast<const uint32_t*>(src)[si];
+    } else {
+      static_cast<uint16_t*>(dst)[di] = static_cast<const uint16_t*>(src)[si];
+    }
+  } else {
+    store_any(dst, di, out_dtype, load_any(src, si, in_dtype));
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void qk_rope_append_kernel(const RopeAppendParams p) {
+  constexpr int VE = 8;
+  constexpr int G = D / VE;          // lanes per row
+  constexpr int RPW = kWave / G;     // rows per wave
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int c = lane % G;
+  const int64_t r = (static_cast<int64_t>(blockIdx.x) * (blockDim.x / kWave) + wave) * RPW + lane / G;
+  const bool live = r < p.n_rows;
+  const int per = p.n_heads + 2 * p.n_kv_heads;
+  int64_t rr = live ? r : 0;
+  const int slot = static_cast<int>(rr % per);
+  rr /= per;
+  const int t = static_cast<int>(rr % p.t_new);
+  const int64_t b = rr / p.t_new;
+  const int pos = p.seqlens[b] + t;
+  const int kind = slot < p.n_heads ? 0 : (slot < p.n_heads + p.n_kv_heads ? 1 : 2);  // q, k, v
+  const int h = kind == 0 ? slot : (kind == 1 ? slot - p.n_heads : slot - p.n_heads - p.n_kv_heads);
+  const void* src = kind == 0 ? p.q : (kind == 1 ? p.k : p.v);
+  const int64_t soff = kind == 0 ? b * p.q_sb + t * p.q_st + h * p.q_sh
+                                 : (kind == 1 ? b * p.k_sb + t * p.k_st + h * p.k_sh
+                                              : b * p.v_sb + t * p.v_st + h * p.v_sh);
+  float x[VE];
+#pragma unroll
+  for (int e = 0; e < VE; ++e) x[e] = live ? load_any(src, soff + c * VE + e, p.q_dtype) : 0.0f;
+  const int row = min(max(pos, 0), p.rot_len - 1);
+  qk_prologue_lanes<G, VE>(x, c, p.cos, p.sin, row, p.rot_dtype, p.scale, p.eps);  // every lane takes part
+  if (!live) return;
+  if (kind == 0) {
+    if (c == 0 && (pos < 0 || pos >= p.rot_len) && p.err != nullptr) atomicOr(p.err, NC_DEVERR_ROPE_RANGE);
+    const int64_t o0 = ((b * p.t_new + t) * p.n_heads + h) * D + c * VE;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) store_any(p.q_out, o0 + e, p.q_dtype, x[e]);
+    return;
+  }
+  if (pos < 0 || pos >= p.t_max) {
+    if (c == 0 && h == 0 && kind == 1 && p.err != nullptr) atomicOr(p.err, NC_DEVERR_OVERFLOW);
+    return;
+  }
+  if (kind == 1) {
+    const int64_t d0 = b * p.kc_sb + static_cast<int64_t>(pos) * p.kc_st + h * p.kc_sh + c * VE;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) store_any(p.kc, d0 + e, p.cache_dtype, x[e]);
+  } else {
+    const int64_t d0 = b * p.vc_sb + static_cast<int64_t>(pos) * p.vc_st + h * p.vc_sh + c * VE;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) copy_elem(p.vc, d0 + e, p.cache_dtype, p.v, soff + c * VE + e, p.q_dtype);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_append(const nc_append_args& a, hipStream_t stream) {
@@ -120,6 +210,39 @@ hipError_t launch_append(const nc_append_args& a, hipStream_t stream) {
     case NC_DTYPE_BF16: hipLaunchKernelGGL(kv_append_kernel<bf16>, grid, block, 0, stream, p); break;
     case NC_DTYPE_F16: hipLaunchKernelGGL(kv_append_kernel<f16>, grid, block, 0, stream, p); break;
     default: hipLaunchKernelGGL(kv_append_kernel<float>, grid, block, 0, stream, p); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_append(const nc_attn_args& a, const nc_qk_prologue& pro, void* q_out, hipStream_t stream) {
+  RopeAppendParams p;
+  p.q = a.q; p.q_out = q_out; p.k = a.k; p.v = a.v;
+  p.kc = static_cast<char*>(a.k_cache); p.vc = static_cast<char*>(a.v_cache);
+  p.seqlens = a.cache_seqlens; p.err = a.error_flag;
+  p.cos = pro.cos; p.sin = pro.sin;
+  p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
+  p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
+  p.v_sb = a.v_stride_b; p.v_st = a.v_stride_t; p.v_sh = a.v_stride_h;
+  p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
+  p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
+  p.n_rows = a.batch * a.t_new * (a.n_heads + 2 * a.n_kv_heads);
+  p.t_new = static_cast<int32_t>(a.t_new);
+  p.t_max = static_cast<int32_t>(a.t_max);
+  p.n_heads = static_cast<int32_t>(a.n_heads);
+  p.n_kv_heads = static_cast<int32_t>(a.n_kv_heads);
+  p.q_dtype = a.q_dtype;
+  p.cache_dtype = a.cache_dtype;
+  p.rot_len = static_cast<int32_t>(pro.rot_len);
+  p.rot_dtype = pro.rot_dtype;
+  p.scale = pro.qk_scale;
+  p.eps = pro.eps;
+  const int64_t rows_per_block = 4 * (kWave / (a.head_dim / 8));
+  const dim3 grid(static_cast<unsigned>((p.n_rows + rows_per_block - 1) / rows_per_block)), block(256);
+  switch (a.head_dim) {
+    case 32: hipLaunchKernelGGL(qk_rope_append_kernel<32>, grid, block, 0, stream, p); break;
+    case 64: hipLaunchKernelGGL(qk_rope_append_kernel<64>, grid, block, 0, stream, p); break;
+    case 128: hipLaunchKernelGGL(qk_rope_append_kernel<128>, grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL(qk_rope_append_kernel<256>, grid, block, 0, stream, p); break;
   }
   return hipGetLastError();
 }

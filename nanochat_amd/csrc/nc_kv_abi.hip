@@ -179,15 +179,14 @@ size_t nc_attn_workspace_bytes(const nc_attn_args* args) {
   return plan.total_bytes;
 }
 
-int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
-  if (args == nullptr) return NC_ERR_NULL_ARG;
-  const nc_attn_args& a = *args;
+namespace {
+
+// Validation shared by both attention entry points; fills the plan.
+int check_attention(const nc_attn_args& a, AttnPlan* plan) {
   if (!a.q || !a.out || !a.k_cache || !a.v_cache || !a.cache_seqlens) return NC_ERR_NULL_ARG;
   if ((a.k == nullptr) != (a.v == nullptr)) return NC_ERR_NULL_ARG;
-  AttnPlan plan;
-  const int st = plan_attention(a, &plan);
+  const int st = plan_attention(a, plan);
   if (st != NC_OK) return st;
-
   const int64_t eb = dtype_bytes(a.cache_dtype);
   if (!aligned16(a.k_cache) || !aligned16(a.v_cache) ||
       !strides16(eb, a.kc_stride_b, a.kc_stride_t, a.kc_stride_h) ||
@@ -203,17 +202,22 @@ int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
        !strides16(eb, a.v_stride_b, a.v_stride_t, a.v_stride_h))) {
     return NC_ERR_ALIGNMENT;
   }
-  if (plan.total_bytes > 0 && (a.workspace == nullptr || a.workspace_bytes < plan.total_bytes ||
-                               !aligned16(a.workspace))) {
-    return NC_ERR_WORKSPACE;
-  }
+  return NC_OK;
+}
 
+AttnScratch carve(const nc_attn_args& a, const AttnPlan& plan) {
   AttnScratch s;
   char* ws = static_cast<char*>(a.workspace);
   s.part_ml = reinterpret_cast<float*>(ws);
   s.part_o = reinterpret_cast<float*>(ws + plan.ml_bytes);
-  hipStream_t hs = static_cast<hipStream_t>(stream);
+  return s;
+}
 
+// Append (unless a prologue already did) and attend: decode kernel for
+// t_new == 1 (append and, with `prologue`, the QK prologue fused), MFMA chunk
+// kernel for chunks, the decode kernel per query otherwise.
+int run_attention(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
+                  const nc_qk_prologue* prologue, hipStream_t hs) {
   bool fused = false;
   if (a.k != nullptr) {
     if (a.t_new == 1 || plan.use_chunk) {
@@ -237,7 +241,72 @@ int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
     if (plan.chunk_splits > 1 && launch_chunk_merge(a, plan, s, hs) != hipSuccess) return NC_ERR_LAUNCH;
     return NC_OK;
   }
-  return launch_decode(a, plan, s, fused, hs) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
+  return launch_decode(a, plan, s, fused, prologue, hs) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
+}
+
+// Bytes of q after the prologue kept in the workspace (t_new > 1).
+size_t rope_q_bytes(const nc_attn_args& a) {
+  if (a.t_new <= 1) return 0;
+  return round256(static_cast<size_t>(a.batch * a.t_new * a.n_heads * a.head_dim) *
+                  static_cast<size_t>(dtype_bytes(a.q_dtype)));
+}
+
+}  // namespace
+
+int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
+  if (args == nullptr) return NC_ERR_NULL_ARG;
+  const nc_attn_args& a = *args;
+  AttnPlan plan;
+  const int st = check_attention(a, &plan);
+  if (st != NC_OK) return st;
+  if (plan.total_bytes > 0 && (a.workspace == nullptr || a.workspace_bytes < plan.total_bytes ||
+                               !aligned16(a.workspace))) {
+    return NC_ERR_WORKSPACE;
+  }
+  return run_attention(a, plan, carve(a, plan), nullptr, static_cast<hipStream_t>(stream));
+}
+
+size_t nc_attn_rope_workspace_bytes(const nc_attn_args* args) {
+  if (args == nullptr) return 0;
+  AttnPlan plan;
+  if (plan_attention(*args, &plan) != NC_OK) return 0;
+  return plan.total_bytes + rope_q_bytes(*args);
+}
+
+int nc_attn_kvcache_rope(const nc_attn_args* args, const nc_qk_prologue* prologue, void* stream) {
+  if (args == nullptr || prologue == nullptr) return NC_ERR_NULL_ARG;
+  const nc_attn_args& a = *args;
+  const nc_qk_prologue& pro = *prologue;
+  if (a.k == nullptr || a.v == nullptr || pro.cos == nullptr || pro.sin == nullptr) return NC_ERR_NULL_ARG;
+  if (pro.rot_len <= 0 || pro.rot_len > INT32_MAX) return NC_ERR_BAD_SHAPE;
+  if (!valid_dtype(pro.rot_dtype)) return NC_ERR_DTYPE;
+  // tables are read with 8-32 byte vector loads at multiples of 4 entries
+  if (!aligned16(pro.cos) || !aligned16(pro.sin) || (a.head_dim / 2 * dtype_bytes(pro.rot_dtype)) % 16 != 0) {
+    return NC_ERR_ALIGNMENT;
+  }
+  AttnPlan plan;
+  const int st = check_attention(a, &plan);
+  if (st != NC_OK) return st;
+  const size_t need = plan.total_bytes + rope_q_bytes(a);
+  if (need > 0 && (a.workspace == nullptr || a.workspace_bytes < need || !aligned16(a.workspace))) {
+    return NC_ERR_WORKSPACE;
+  }
+  const int64_t rows = a.batch * a.t_new * (a.n_heads + 2 * a.n_kv_heads);
+  if (rows / 4 > INT32_MAX) return NC_ERR_BAD_SHAPE;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const AttnScratch s = carve(a, plan);
+  if (a.t_new == 1) return run_attention(a, plan, s, &pro, hs);
+  // t_new > 1: prologue kernel (q -> workspace, k/v -> cache), then attention without append
+  void* q_out = static_cast<char*>(a.workspace) + plan.total_bytes;
+  if (launch_rope_append(a, pro, q_out, hs) != hipSuccess) return NC_ERR_LAUNCH;
+  nc_attn_args b = a;
+  b.q = q_out;
+  b.q_stride_h = a.head_dim;
+  b.q_stride_t = a.n_heads * a.head_dim;
+  b.q_stride_b = a.t_new * a.n_heads * a.head_dim;
+  b.k = nullptr;
+  b.v = nullptr;
+  return run_attention(b, plan, s, nullptr, hs);
 }
 
 }  // extern "C"

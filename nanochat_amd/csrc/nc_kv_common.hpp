@@ -138,6 +138,21 @@ __device__ __forceinline__ uint4 load_as_cache_vec(const void* base, int64_t off
   }
 }
 
+// VEC fp32 values -> one 16-byte vector of cache type T (RNE, as copy_ rounds).
+template <typename T>
+__device__ __forceinline__ uint4 pack_cache_vec(const float* x) {
+  if constexpr (elem<T>::kBytes == 4) {
+    return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3]));
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = static_cast<uint32_t>(narrow<T>::run(x[2 * i])) | (static_cast<uint32_t>(narrow<T>::run(x[2 * i + 1])) << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane sums inside groups of N consecutive lanes (N a power of two,
 // N <= 64).  N <= 16 stays inside a DPP row: quad_perm swaps for 1 and 2,
@@ -162,6 +177,89 @@ __device__ __forceinline__ float group_sum(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// VE consecutive table entries starting at element `off` (runtime dtype),
+// with 8/16/32-byte vector loads (tables are 16-byte aligned and the offsets
+// are multiples of VE).
+template <int VE>
+__device__ __forceinline__ void load_table_vec(const void* tab, int64_t off, int dtype, float (&out)[VE]) {
+  if (dtype == NC_DTYPE_F32) {
+    const float4* p4 = reinterpret_cast<const float4*>(static_cast<const float*>(tab) + off);
+#pragma unroll
+    for (int i = 0; i < VE / 4; ++i) {
+      const float4 v = p4[i];
+      out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
+    }
+  } else {
+    const uint16_t* p16 = static_cast<const uint16_t*>(tab) + off;
+    uint32_t w[VE / 2];
+    if constexpr (VE == 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p16);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(p16);
+      w[0] = v.x; w[1] = v.y;
+    }
+#pragma unroll
+    for (int i = 0; i < VE / 2; ++i) {
+      if (dtype == NC_DTYPE_BF16) {
+        out[2 * i] = __uint_as_float(w[i] << 16);
+        out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+      } else {
+        out[2 * i] = half_bits_to_f32(static_cast<uint16_t>(w[i] & 0xffffu));
+        out[2 * i + 1] = half_bits_to_f32(static_cast<uint16_t>(w[i] >> 16));
+      }
+    }
+  }
+}
+
+// QK prologue of one head vector (nanochat/gpt.py:98-102): rotary with this
+// lane's table entries cs/sn (y1 = x1 cos + x2 sin, y2 = -x1 sin + x2 cos
+// over the halves [0, D/2), [D/2, D); gpt.py:57-63), RMS norm over D with eps
+// (gpt.py:42-43), times `scale`.  The vector is held VE values per lane by G
+// consecutive lanes (lane c of the group: dims [VE c, VE c + VE); its table
+// entries are columns [VE (c mod G/2), +VE)), so the rotary partner of a lane
+// is lane c ^ G/2 and the norm is a G-lane sum.  fp32 throughout; every lane
+// of the wave must take part (cross-lane exchange).
+template <int G, int VE>
+__device__ __forceinline__ void qk_prologue_apply(float (&x)[VE], int c, const float (&cs)[VE],
+                                                  const float (&sn)[VE], float scale, float eps) {
+  static_assert(G >= 2 && (G & (G - 1)) == 0, "lanes per head vector");
+  constexpr int D = G * VE;
+  float y[VE];
+#pragma unroll
+  for (int e = 0; e < VE; ++e) y[e] = __shfl_xor(x[e], G / 2, kWave);
+  const bool first = c < G / 2;
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < VE; ++e) {
+    x[e] = first ? __builtin_fmaf(x[e], cs[e], y[e] * sn[e]) : __builtin_fmaf(x[e], cs[e], -(y[e] * sn[e]));
+    ss = __builtin_fmaf(x[e], x[e], ss);
+  }
+  ss = group_sum<G>(ss);
+  const float inv = scale / sqrtf(ss * (1.0f / D) + eps);
+#pragma unroll
+  for (int e = 0; e < VE; ++e) x[e] *= inv;
+}
+
+// Same, loading the table entries of table row `row` first.
+template <int G, int VE>
+__device__ __forceinline__ void qk_prologue_lanes(float (&x)[VE], int c, const void* cos_tab, const void* sin_tab,
+                                                  int64_t row, int tab_dtype, float scale, float eps) {
+  constexpr int D = G * VE;
+  float cs[VE], sn[VE];
+  const int64_t off = row * (D / 2) + static_cast<int64_t>(c % (G / 2)) * VE;
+  load_table_vec<VE>(cos_tab, off, tab_dtype, cs);
+  load_table_vec<VE>(sin_tab, off, tab_dtype, sn);
+  qk_prologue_apply<G, VE>(x, c, cs, sn, scale, eps);
+}
+
+// Round to a storage dtype and back (the value a tensor of that dtype holds).
+__device__ __forceinline__ float round_to(float x, int dtype) {
+  if (dtype == NC_DTYPE_BF16) return __uint_as_float(static_cast<uint32_t>(f32_to_bf16_rne(x)) << 16);
+  if (dtype == NC_DTYPE_F16) return half_bits_to_f32(f32_to_f16_rne(x));
+  return x;
+}
 
 // Division of integers in [0, 2^31) by a divisor fixed for the whole launch,
 // as a multiply-high and a shift (Granlund & Montgomery, "Division by

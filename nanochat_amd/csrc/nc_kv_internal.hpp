@@ -36,8 +36,12 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan);
 
 hipError_t launch_append(const nc_append_args& a, hipStream_t stream);
 hipError_t launch_fanout(const nc_fanout_args& a, int unit_bytes, hipStream_t stream);
+// prologue != nullptr: the fused QK prologue on q and the appended k (t_new == 1 with k/v).
 hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
-                         bool fused_append, hipStream_t stream);
+                         bool fused_append, const nc_qk_prologue* prologue, hipStream_t stream);
+// QK prologue for t_new > 1: q -> q_out (contiguous (B, T, H, D), q's dtype), k (transformed) and
+// v appended into the cache.
+hipError_t launch_rope_append(const nc_attn_args& a, const nc_qk_prologue& pro, void* q_out, hipStream_t stream);
 
 bool decode_supports(int cache_dtype, int64_t head_dim);
 bool chunk_supports(const nc_attn_args& a);

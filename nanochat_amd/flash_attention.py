@@ -67,20 +67,14 @@ def _dtype_code(t: torch.Tensor, name: str) -> int:
     return code
 
 
-def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
-                            causal=False, window_size=(-1, -1), *, keys_per_split: int = 0):
-    """Append k/v into the cache in place, then attend (see the module docstring).
-
-    q: (B, T_new, H, D); k_cache, v_cache: (B, T_max, H_kv, D);
-    k, v: (B, T_new, H_kv, D) or None; cache_seqlens: (B,) int32 on the GPU.
-    Returns (B, T_new, H, D) in q's dtype.
-    """
+def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_size, keys_per_split):
+    """Validate the arguments of one attention call and fill nc_attn_args (workspace left empty)."""
     if cache_seqlens is None:
-        raise ValueError("flash_attn_with_kvcache: cache_seqlens is required")
+        raise ValueError(f"{name}: cache_seqlens is required")
     if (k is None) != (v is None):
-        raise ValueError("flash_attn_with_kvcache: pass both k and v, or neither")
+        raise ValueError(f"{name}: pass both k and v, or neither")
     if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
-        raise ValueError("flash_attn_with_kvcache: q, k_cache, v_cache must be 4-D (B, T, H, D)")
+        raise ValueError(f"{name}: q, k_cache, v_cache must be 4-D (B, T, H, D)")
     B, T_new, H, D = q.shape
     Bc, T_max, H_kv, Dc = k_cache.shape
     if tuple(v_cache.shape) != (Bc, T_max, H_kv, Dc):
@@ -99,14 +93,13 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     if k_cache.dtype != v_cache.dtype:
         raise TypeError("k_cache and v_cache must have the same dtype")
     tensors = [q, k_cache, v_cache, cache_seqlens] + ([k, v] if k is not None else [])
-    dev = _require_gpu("flash_attn_with_kvcache", *tensors)
-    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("k", k), ("v", v)):
+    dev = _require_gpu(name, *tensors)
+    for tname, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("k", k), ("v", v)):
         if t is not None and t.stride(-1) != 1:
-            raise ValueError(f"{name} must be contiguous in its last (head_dim) dimension")
+            raise ValueError(f"{tname} must be contiguous in its last (head_dim) dimension")
     if not cache_seqlens.is_contiguous():
         cache_seqlens = cache_seqlens.contiguous()
 
-    L = _ext.lib()
     out = torch.empty((B, T_new, H, D), dtype=q.dtype, device=dev)
     window = int(window_size[0]) if window_size is not None else -1
     a = _ext.AttnArgs()
@@ -130,18 +123,87 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     a.q_dtype = _dtype_code(q, "q")
     a.cache_dtype = _dtype_code(k_cache, "k_cache")
     a.keys_per_split = int(keys_per_split)
-    ref = ctypes.byref(a)
-    need = L.nc_attn_workspace_bytes(ref)
-    stream = _ext.stream_handle(dev)
+    return a, out, dev, cache_seqlens
+
+
+def _attach_workspace(a, dev, stream, need):
     ws = _ext.workspace(dev, stream, need)
     if ws is not None:
         a.workspace = ws.data_ptr()
         a.workspace_bytes = ws.numel()
-    _ext.check(L.nc_attn_kvcache(ref, stream), "nc_attn_kvcache")
+
+
+def _check_device_errors(name, dev):
     if _CHECK_ERRORS:
         bits = _ext.read_and_clear_device_errors(dev)
         if bits & _ext.NC_DEVERR_OVERFLOW:
-            raise RuntimeError("flash_attn_with_kvcache: cache_seqlens + T_new exceeds the cache length")
+            raise RuntimeError(f"{name}: cache_seqlens + T_new exceeds the cache length")
+        if bits & _ext.NC_DEVERR_ROPE_RANGE:
+            raise RuntimeError(f"{name}: a position is beyond the rotary tables")
+
+
+def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
+                            causal=False, window_size=(-1, -1), *, keys_per_split: int = 0):
+    """Append k/v into the cache in place, then attend (see the module docstring).
+
+    q: (B, T_new, H, D); k_cache, v_cache: (B, T_max, H_kv, D);
+    k, v: (B, T_new, H_kv, D) or None; cache_seqlens: (B,) int32 on the GPU.
+    Returns (B, T_new, H, D) in q's dtype.
+    """
+    a, out, dev, _ = _attn_call("flash_attn_with_kvcache", q, k_cache, v_cache, k, v, cache_seqlens, causal,
+                                window_size, keys_per_split)
+    L = _ext.lib()
+    ref = ctypes.byref(a)
+    stream = _ext.stream_handle(dev)
+    _attach_workspace(a, dev, stream, L.nc_attn_workspace_bytes(ref))
+    _ext.check(L.nc_attn_kvcache(ref, stream), "nc_attn_kvcache")
+    _check_device_errors("flash_attn_with_kvcache", dev)
+    return out
+
+
+def flash_attn_with_kvcache_rope(q, k_cache, v_cache, k, v, cache_seqlens, cos, sin, causal=True,
+                                 window_size=(-1, -1), *, qk_scale: float = 1.2, eps=None,
+                                 keys_per_split: int = 0):
+    """flash_attn_with_kvcache with nanochat's QK prologue fused (nanochat/gpt.py:98-102).
+
+    q and k are the raw projections; inside the call each token t of row b is
+    rotated with table row cache_seqlens[b] + t of cos/sin (the model's
+    (1, T_rot, 1, D/2) buffers or (T_rot, D/2) tables), RMS-normalised over D
+    with `eps` (default torch.finfo(q.dtype).eps, F.rms_norm's default) and
+    scaled by qk_scale; k is appended in that form, v as given.  Equivalent to
+    rotary + norm + scale in torch followed by flash_attn_with_kvcache, with
+    one rounding instead of one per op.
+    """
+    if k is None or v is None:
+        raise ValueError("flash_attn_with_kvcache_rope: k and v are required")
+    D = q.shape[-1]
+    if D % 2 != 0:
+        raise ValueError("flash_attn_with_kvcache_rope: head_dim must be even")
+    cos2 = cos.reshape(-1, cos.shape[-1])
+    sin2 = sin.reshape(-1, sin.shape[-1])
+    if cos2.shape != sin2.shape or cos2.shape[1] != D // 2:
+        raise ValueError(f"rotary tables must be (T, {D // 2}); got {tuple(cos.shape)}, {tuple(sin.shape)}")
+    if cos2.dtype != sin2.dtype:
+        raise TypeError("cos and sin must have the same dtype")
+    if not cos2.is_contiguous() or cos2.data_ptr() % 16 != 0:
+        cos2 = cos2.clone(memory_format=torch.contiguous_format)
+    if not sin2.is_contiguous() or sin2.data_ptr() % 16 != 0:
+        sin2 = sin2.clone(memory_format=torch.contiguous_format)
+    a, out, dev, _ = _attn_call("flash_attn_with_kvcache_rope", q, k_cache, v_cache, k, v, cache_seqlens, causal,
+                                window_size, keys_per_split)
+    _require_gpu("flash_attn_with_kvcache_rope", cos2, sin2)
+    pro = _ext.QKPrologue()
+    pro.cos, pro.sin = cos2.data_ptr(), sin2.data_ptr()
+    pro.rot_len = cos2.shape[0]
+    pro.rot_dtype = _dtype_code(cos2, "cos")
+    pro.qk_scale = float(qk_scale)
+    pro.eps = float(torch.finfo(q.dtype).eps if eps is None else eps)
+    L = _ext.lib()
+    ref = ctypes.byref(a)
+    stream = _ext.stream_handle(dev)
+    _attach_workspace(a, dev, stream, L.nc_attn_rope_workspace_bytes(ref))
+    _ext.check(L.nc_attn_kvcache_rope(ref, ctypes.byref(pro), stream), "nc_attn_kvcache_rope")
+    _check_device_errors("flash_attn_with_kvcache_rope", dev)
     return out
 
 
@@ -188,4 +250,5 @@ def kv_append(k_cache, v_cache, k, v, cache_seqlens):
 flash_attn = SimpleNamespace(
     flash_attn_func=flash_attn_func,
     flash_attn_with_kvcache=flash_attn_with_kvcache,
+    flash_attn_with_kvcache_rope=flash_attn_with_kvcache_rope,
 )

@@ -8,7 +8,10 @@ attention goes through nanochat_amd.flash_attention (libnc_kv.so):
 
   - CausalSelfAttention with a cache (nanochat/gpt.py:82-126): q/k/v
     projections, gated value embeddings, rotary, QK RMS norm, x1.2, then
-    flash_attn_with_kvcache; the last layer advances the cache by T.
+    flash_attn_with_kvcache; the last layer advances the cache by T.  On the
+    GPU the rotary/norm/x1.2 prologue runs inside the cache call
+    (flash_attn_with_kvcache_rope, positions from cache_seqlens) unless
+    GPT.fused_qk_prologue is False; on the CPU the op-by-op sequence runs.
   - GPT.forward (nanochat/gpt.py:416-481): rotary offset T0 = kv_cache.get_pos(),
     smear with the cached previous embedding, resid/x0 lambdas, backout at
     n_layer // 2, final norm, lm_head, softcap 15.
@@ -19,6 +22,7 @@ Training (loss, optimizer set-up, FLOP counts) is not part of this build.
 from __future__ import annotations
 
 from dataclasses import dataclass
+from typing import NamedTuple
 
 import torch
 import torch.nn as nn
@@ -63,6 +67,15 @@ def rotate_half_pairs(x, cos, sin):
     return torch.cat([a * cos + b * sin, a * (-sin) + b * cos], 3)
 
 
+def rotary_tables(seq_len, head_dim, base=100000, device=None, dtype=torch.float32):
+    """cos/sin tables (seq_len, head_dim/2) of t * base^(-2i/D), built in fp32 and cast to dtype."""
+    channels = torch.arange(0, head_dim, 2, dtype=torch.float32, device=device)
+    inv_freq = 1.0 / (base ** (channels / head_dim))
+    t = torch.arange(seq_len, dtype=torch.float32, device=device)
+    freqs = torch.outer(t, inv_freq)
+    return freqs.cos().to(dtype), freqs.sin().to(dtype)
+
+
 def window_sizes(config: GPTConfig):
     """Per-layer (left, right) windows: L = sequence_len, S = ceil(seq/4 to 128); last layer L."""
     pattern = config.window_pattern.upper()
@@ -73,6 +86,12 @@ def window_sizes(config: GPTConfig):
     sizes = [(long_w if pattern[i % len(pattern)] == "L" else short_w, 0) for i in range(config.n_layer)]
     sizes[-1] = (long_w, 0)
     return sizes
+
+
+class FusedRope(NamedTuple):
+    """Whole rotary tables handed to attention when the QK prologue runs inside the cache call."""
+    cos: torch.Tensor
+    sin: torch.Tensor
 
 
 class CausalSelfAttention(nn.Module):
@@ -101,6 +120,15 @@ class CausalSelfAttention(nn.Module):
             ve = ve.view(B, T, self.n_kv_head, self.head_dim)
             gate = 3 * torch.sigmoid(self.ve_gate(x[..., :self.ve_gate_channels]))
             v = v + gate.unsqueeze(-1) * ve
+        if isinstance(cos_sin, FusedRope):
+            # rotary at each row's cache position + QK norm + x1.2 inside the attention call
+            k_cache, v_cache = kv_cache.get_layer_cache(self.layer_idx)
+            y = flash_attn.flash_attn_with_kvcache_rope(q, k_cache, v_cache, k, v, kv_cache.cache_seqlens,
+                                                        cos_sin.cos, cos_sin.sin, causal=True,
+                                                        window_size=window_size)
+            if self.layer_idx == kv_cache.n_layers - 1:
+                kv_cache.advance(T)
+            return self.c_proj(y.contiguous().view(B, T, -1))
         cos, sin = cos_sin
         q, k = rotate_half_pairs(q, cos, sin), rotate_half_pairs(k, cos, sin)
         q, k = rms(q), rms(k)
@@ -171,11 +199,7 @@ class GPT(nn.Module):
     def _rotary_tables(self, seq_len, head_dim, base=100000, device=None):
         if device is None:
             device = self.transformer.wte.weight.device
-        channels = torch.arange(0, head_dim, 2, dtype=torch.float32, device=device)
-        inv_freq = 1.0 / (base ** (channels / head_dim))
-        t = torch.arange(seq_len, dtype=torch.float32, device=device)
-        freqs = torch.outer(t, inv_freq)
-        cos, sin = freqs.cos().to(self.compute_dtype), freqs.sin().to(self.compute_dtype)
+        cos, sin = rotary_tables(seq_len, head_dim, base, device, self.compute_dtype)
         return cos[None, :, None, :], sin[None, :, None, :]
 
     @torch.no_grad()
@@ -215,12 +239,21 @@ class GPT(nn.Module):
     def get_device(self):
         return self.transformer.wte.weight.device
 
+    # With a KV cache on the GPU, rotary + QK norm + x1.2 run inside the attention call
+    # (flash_attn_with_kvcache_rope), which takes positions from the device-side
+    # cache_seqlens: no get_pos() host sync and ~10 fewer launches per layer.  False
+    # keeps the reference's op-by-op sequence.
+    fused_qk_prologue = True
+
     def forward(self, idx, kv_cache=None):
         """Logits (B, T, vocab) in fp32.  With a cache, attention appends into it."""
         B, T = idx.size()
         assert T <= self.cos.size(1), f"Sequence length grew beyond the rotary table: {T} > {self.cos.size(1)}"
-        T0 = 0 if kv_cache is None else kv_cache.get_pos()
-        cos_sin = self.cos[:, T0:T0 + T], self.sin[:, T0:T0 + T]
+        if kv_cache is not None and self.fused_qk_prologue and idx.is_cuda:
+            cos_sin = FusedRope(self.cos, self.sin)  # positions beyond the table set a device flag
+        else:
+            T0 = 0 if kv_cache is None else kv_cache.get_pos()
+            cos_sin = self.cos[:, T0:T0 + T], self.sin[:, T0:T0 + T]
         x = self.transformer.wte(idx)
         x = x.to(self.compute_dtype)
         x = rms(x)

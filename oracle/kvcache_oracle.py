@@ -14,6 +14,11 @@ It restates, with the same torch operations the reference uses:
                                uniform batch this is the reference fallback itself
   - KVCache                    nanochat/engine.py:82-137
   - compute_window_sizes       nanochat/gpt.py:285-312
+  - rotary / qk_prologue       nanochat/gpt.py:57-63 (apply_rotary_emb), :42-43
+                               (norm), :98-102 (rotary, QK norm, x1.2) with each
+                               row's own position s_b (the fused prologue's contract;
+                               the reference slices the table at row 0's position)
+  - rotary_tables              nanochat/gpt.py:268-283
 The pins for each function (brute force, closed forms, the reference's own
 known-answer test) live in tests/test_oracle.py.
 
@@ -177,3 +182,34 @@ def decode_bytes(seqlens, n_layers, n_heads, n_kv_heads, head_dim, elem_bytes, w
 
 def softmax_scale(head_dim):
     return 1.0 / math.sqrt(head_dim)
+
+
+def rotary_tables(seq_len, head_dim, base=100000, dtype=torch.float32):
+    """nanochat/gpt.py:268-283: cos/sin of t * base^(-2i/D), shape (seq_len, D/2), cast to dtype."""
+    channel_range = torch.arange(0, head_dim, 2, dtype=torch.float32)
+    inv_freq = 1.0 / (base ** (channel_range / head_dim))
+    t = torch.arange(seq_len, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    return freqs.cos().to(dtype), freqs.sin().to(dtype)
+
+
+def rotary(x, cos, sin):
+    """nanochat/gpt.py:57-63 on (B, T, H, D) with cos/sin broadcastable to (B, T, 1, D/2)."""
+    d = x.shape[3] // 2
+    x1, x2 = x[..., :d], x[..., d:]
+    return torch.cat([x1 * cos + x2 * sin, x1 * (-sin) + x2 * cos], 3)
+
+
+def qk_prologue(x, cos_tab, sin_tab, positions, scale=1.2, eps=None):
+    """Rotary at each row's positions, RMS norm over D, times scale (nanochat/gpt.py:98-102).
+
+    x is (B, T, H, D); token t of row b uses table row positions[b] + t.  Every
+    operation runs in x's dtype, as the reference's do in COMPUTE_DTYPE.
+    """
+    T = x.shape[1]
+    idx = positions.long()[:, None] + torch.arange(T)[None, :]
+    cos = cos_tab[idx][:, :, None, :].to(x.dtype)
+    sin = sin_tab[idx][:, :, None, :].to(x.dtype)
+    y = rotary(x, cos, sin)
+    y = F.rms_norm(y, (y.size(-1),), eps=eps)
+    return y * scale

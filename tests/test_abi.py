@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_struct_layouts_match_header_field_order():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     for cname, pystruct in (("nc_append_args", _ext.AppendArgs), ("nc_fanout_args", _ext.FanoutArgs),
-                            ("nc_attn_args", _ext.AttnArgs)):
+                            ("nc_attn_args", _ext.AttnArgs), ("nc_qk_prologue", _ext.QKPrologue)):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), text, flags=re.S).group(1)
         names = []
         for decl in body.split(";"):

@@ -201,3 +201,32 @@ def test_c3_engine_generate_d24():
         assert len(column) == 16 and all(0 <= t < 32768 for t in column)
         steps += 1
     assert steps == 128
+
+
+# ---- the fused QK prologue in the model (rotary/norm/x1.2 inside the cache call) ----
+def test_fused_and_op_by_op_prologue_agree_in_the_model():
+    """GPT.forward with a cache (C1 model, perturbed weights, fp32 compute, bf16 cache): logits of a prefill
+    and three decode steps through flash_attn_with_kvcache_rope equal the reference's op-by-op prologue
+    within bf16 noise, and the caches agree."""
+    model = c1_model("perturbed").to(DEV)
+    m = model.config
+    prompt = GOLDEN["prompt"][:32]
+    runs = []
+    for fused in (True, False):
+        model.fused_qk_prologue = fused
+        kv = KVCache(batch_size=1, num_heads=m.n_kv_head, seq_len=40, head_dim=m.n_embd // m.n_head,
+                     num_layers=m.n_layer, device=DEV, dtype=torch.bfloat16)
+        logits = []
+        with torch.inference_mode():
+            ids = torch.tensor([prompt], device=DEV)
+            for _ in range(4):
+                out = model.forward(ids, kv_cache=kv)[:, -1, :]
+                logits.append(out.float())
+                ids = torch.argmax(out, dim=-1, keepdim=True)
+        runs.append((logits, kv))
+    model.fused_qk_prologue = True
+    for a, b in zip(runs[0][0], runs[1][0]):
+        assert float((a - b).abs().max()) <= 2e-2 * float(b.abs().max()) + 1e-3
+    assert torch.equal(runs[0][1].cache_seqlens, runs[1][1].cache_seqlens)
+    dk = (runs[0][1].k_cache.float() - runs[1][1].k_cache.float()).abs().max()
+    assert float(dk) <= 0.05

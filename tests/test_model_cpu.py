@@ -119,3 +119,12 @@ def test_calculator_tool():
     assert eng.use_calculator("'strawberry'.count('r')") == 3
     for bad in ("2**10", "__import__('os')", "1/0", "open('x').count('a')", "'a'.upper()", "x.count('a')"):
         assert eng.use_calculator(bad) is None, bad
+
+
+def test_model_rotary_tables_equal_oracle():
+    """nanochat_amd.gpt.rotary_tables (the fused prologue's tables) is the restated gpt.py:268-283."""
+    from oracle import kvcache_oracle as orc
+    for dtype in (torch.float32, torch.bfloat16):
+        c1, s1 = gpt.rotary_tables(300, 128, dtype=dtype)
+        c2, s2 = orc.rotary_tables(300, 128, dtype=dtype)
+        assert torch.equal(c1, c2) and torch.equal(s1, s2)

@@ -252,3 +252,70 @@ def test_decode_bytes_closed_form():
     # a window caps the keys at w + 1
     assert orc.decode_bytes([100], 1, 1, 1, 128, 2, windows=[9]) == 512 * 10 + 512 + 512
     assert math.isclose(orc.softmax_scale(128), 128 ** -0.5)
+
+
+# ---- the QK prologue (rotary, RMS norm, x1.2): nanochat/gpt.py:42-43,57-63,98-102,268-283 ----
+def _complex_rotary(x, cos, sin):
+    """Closed form: (x1 + i x2) * exp(-i theta) with cos/sin of theta."""
+    d = x.shape[3] // 2
+    z = torch.complex(x[..., :d].double(), x[..., d:].double()) * torch.complex(cos.double(), -sin.double())
+    return torch.cat([z.real, z.imag], 3)
+
+
+def test_rotary_tables_closed_form():
+    cos, sin = orc.rotary_tables(64, 16, dtype=torch.float64)
+    assert cos.shape == (64, 8)
+    assert torch.equal(cos[0], torch.ones(8, dtype=torch.float64)) and torch.equal(sin[0], torch.zeros(8, dtype=torch.float64))
+    t, i = 37, 3
+    theta = t * 100000.0 ** (-(2 * i) / 16)
+    assert abs(cos[t, i].item() - math.cos(theta)) < 1e-6 and abs(sin[t, i].item() - math.sin(theta)) < 1e-6
+
+
+def test_rotary_equals_complex_rotation_and_preserves_pair_norms():
+    g = gen(60)
+    x = torch.randn(2, 5, 3, 16, generator=g, dtype=torch.float64)
+    cos_t, sin_t = orc.rotary_tables(40, 16, dtype=torch.float64)
+    pos = torch.tensor([0, 31])
+    idx = pos[:, None] + torch.arange(5)[None, :]
+    cos, sin = cos_t[idx][:, :, None, :], sin_t[idx][:, :, None, :]
+    y = orc.rotary(x, cos, sin)
+    assert torch.allclose(y, _complex_rotary(x, cos, sin), atol=1e-12)
+    pair = lambda z: z[..., :8] ** 2 + z[..., 8:] ** 2  # noqa: E731
+    assert torch.allclose(pair(y), pair(x), atol=1e-12)
+    assert torch.allclose(y[0, 0], x[0, 0])  # position 0 is the identity
+    # rotations compose: angle a then angle b equals angle a + b (tables are built in fp32, as the reference's)
+    a, b = 3, 11
+    ya = orc.rotary(x, cos_t[a], sin_t[a])
+    assert torch.allclose(orc.rotary(ya, cos_t[b], sin_t[b]), orc.rotary(x, cos_t[a + b], sin_t[a + b]), atol=1e-5)
+
+
+def test_qk_prologue_normalises_and_scales():
+    g = gen(61)
+    x = torch.randn(3, 4, 2, 32, generator=g, dtype=torch.float64) * 3.0
+    cos_t, sin_t = orc.rotary_tables(64, 32, dtype=torch.float64)
+    pos = torch.tensor([0, 5, 40])
+    eps = 1e-3
+    y = orc.qk_prologue(x, cos_t, sin_t, pos, scale=1.2, eps=eps)
+    idx = pos[:, None] + torch.arange(4)[None, :]
+    r = _complex_rotary(x, cos_t[idx][:, :, None, :], sin_t[idx][:, :, None, :])
+    ms = (r ** 2).mean(-1, keepdim=True)
+    assert torch.allclose(y, 1.2 * r / torch.sqrt(ms + eps), atol=1e-12)
+    assert torch.allclose((y / 1.2).pow(2).mean(-1), (ms / (ms + eps)).squeeze(-1), atol=1e-12)
+
+
+def test_qk_prologue_detects_planted_sign_mistake(monkeypatch):
+    g = gen(62)
+    x = torch.randn(1, 3, 1, 8, generator=g, dtype=torch.float64)
+    cos_t, sin_t = orc.rotary_tables(16, 8, dtype=torch.float64)
+    pos = torch.tensor([4])
+    idx = pos[:, None] + torch.arange(3)[None, :]
+    ref = _complex_rotary(x, cos_t[idx][:, :, None, :], sin_t[idx][:, :, None, :])
+
+    def wrong(x, cos, sin):
+        d = x.shape[3] // 2
+        x1, x2 = x[..., :d], x[..., d:]
+        return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], 3)  # rotation the other way
+
+    monkeypatch.setattr(orc, "rotary", wrong)
+    out = orc.rotary(x, cos_t[idx][:, :, None, :], sin_t[idx][:, :, None, :])
+    assert not torch.allclose(out, ref, atol=1e-6)
