@@ -375,9 +375,45 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
         model.forward(ids, kv_cache=kv)
     kv.cache_seqlens.fill_(P)
     res["fused_graph"] = timed(graph.replay, steps)
-    return {"config": "e2e", "workload": f"d20 GPT decode step (random init, bf16, SSSL), B={B} at position {P}, "
-                                         f"{steps} steps", **{k + "_ms_per_step": round(v, 4) for k, v in res.items()},
-            "tokens_per_s_fused_graph": round(B / (res["fused_graph"] * 1e-3), 1)}
+    out = {"config": "e2e", "workload": f"d20 GPT decode step (random init, bf16, SSSL), B={B} at position {P}, "
+                                        f"{steps} steps", **{k + "_ms_per_step": round(v, 4) for k, v in res.items()},
+           "tokens_per_s_fused_graph": round(B / (res["fused_graph"] * 1e-3), 1)}
+    del graph, kv, model
+    torch.cuda.empty_cache()
+
+    # C3-shaped Engine.generate: d24, 1024-token prompt, 16 samples, `steps` tokens (wall clock, host loop included)
+    from nanochat_amd.engine import Engine
+
+    class _Tok:
+        def encode_special(self, s):
+            return 32759 + ["<|bos|>", "<|user_start|>", "<|user_end|>", "<|assistant_start|>", "<|assistant_end|>",
+                            "<|python_start|>", "<|python_end|>", "<|output_start|>", "<|output_end|>"].index(s)
+
+        def get_bos_token_id(self):
+            return 32759
+
+    cfg3 = GPTConfig(sequence_len=2048, vocab_size=32768, n_layer=24, n_head=12, n_kv_head=12, n_embd=1536)
+    model3 = build_model(cfg3, dev, compute_dtype=torch.bfloat16, seed=0)
+    g3 = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, 32759, (1024,), generator=g3).tolist()
+    for name, fused, use_graph in (("op_by_op", False, False), ("fused", True, False), ("fused_graph", True, True)):
+        model3.fused_qk_prologue = fused
+        engine = Engine(model3, _Tok(), use_graph=use_graph)
+        for _ in engine.generate(prompt, num_samples=16, max_tokens=4, temperature=1.0, seed=0):
+            pass  # warm up
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        n = 0
+        for _ in engine.generate(prompt, num_samples=16, max_tokens=steps, temperature=1.0, seed=0):
+            n += 1
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        out[f"engine_c3_{name}_ms_per_step"] = round(dt * 1e3 / n, 4)
+        out[f"engine_c3_{name}_tokens_per_s"] = round(16 * n / dt, 1)
+    model3.fused_qk_prologue = True
+    out["engine_c3_workload"] = (f"Engine.generate d24 (random init, bf16), 1024-token prompt, 16 samples, {steps} "
+                                 "tokens incl. prefill + fan-out; wall clock")
+    return out
 
 
 def main() -> int:

@@ -179,12 +179,59 @@ class RowState:
         self.completed = False
 
 
+class GraphDecodeStep:
+    """One decode forward of (B, 1) token ids replayed from a HIP graph.
+
+    The first call runs eagerly on a side stream (library handles and the
+    attention workspace of that stream get created); the second captures the
+    forward and replays it; later calls only copy the ids in and replay.  The
+    forward must not synchronise the host, which holds when the model runs the
+    QK prologue inside the attention call (positions come from the device-side
+    cache_seqlens; the cache advances in place).  The returned logits are the
+    graph's output buffer, overwritten by the next call.
+    """
+
+    def __init__(self, model, cache, batch, device):
+        self.model, self.cache = model, cache
+        self.ids = torch.zeros((batch, 1), dtype=torch.long, device=device)
+        self.stream = torch.cuda.Stream(device=device)
+        self.graph = None
+        self.logits = None
+        self.calls = 0
+
+    def __call__(self, ids):
+        main = torch.cuda.current_stream()
+        self.ids.copy_(ids)
+        self.stream.wait_stream(main)
+        if self.graph is None and self.calls == 0:
+            with torch.cuda.stream(self.stream):
+                out = self.model.forward(self.ids, kv_cache=self.cache)[:, -1, :]
+        else:
+            if self.graph is None:
+                self.graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.graph, stream=self.stream):
+                    self.logits = self.model.forward(self.ids, kv_cache=self.cache)[:, -1, :]
+            with torch.cuda.stream(self.stream):
+                self.graph.replay()
+            out = self.logits
+        main.wait_stream(self.stream)
+        self.calls += 1
+        return out
+
+
 class Engine:
     """Batched generation with one prefill and a fanned-out KV cache."""
 
-    def __init__(self, model, tokenizer):
+    def __init__(self, model, tokenizer, use_graph=None):
         self.model = model
         self.tokenizer = tokenizer
+        # None: replay decode steps from a HIP graph whenever the model runs the fused QK prologue on the GPU
+        self.use_graph = use_graph
+
+    def _graph_decode(self, device):
+        if device.type != "cuda" or not getattr(self.model, "fused_qk_prologue", False):
+            return False
+        return True if self.use_graph is None else bool(self.use_graph)
 
     @torch.inference_mode()
     def generate(self, tokens, num_samples=1, max_tokens=None, temperature=1.0, top_k=None, seed=42):
@@ -212,6 +259,7 @@ class Engine:
         cache.prefill(prefill_cache)
         del prefill_cache
 
+        step = GraphDecodeStep(self.model, cache, num_samples, device) if self._graph_decode(device) else None
         rows = [RowState(tokens.copy()) for _ in range(num_samples)]
         generated = 0
         while True:
@@ -246,7 +294,7 @@ class Engine:
             yield column, masks
             generated += 1
             ids = torch.tensor(column, dtype=torch.long, device=device).unsqueeze(1)
-            logits = self.model.forward(ids, kv_cache=cache)[:, -1, :]
+            logits = step(ids) if step is not None else self.model.forward(ids, kv_cache=cache)[:, -1, :]
 
     def generate_batch(self, tokens, num_samples=1, **kwargs):
         """Final sequences (terminal tokens dropped) and masks; nanochat/engine.py:282-304."""

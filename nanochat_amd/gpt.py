@@ -263,13 +263,19 @@ class GPT(nn.Module):
             x = torch.cat([x[:, :1], x[:, 1:] + gate * x[:, :-1]], dim=1)
         else:
             prev = kv_cache.prev_embedding
-            kv_cache.prev_embedding = x[:, -1:, :]
+            last = x[:, -1:, :]
             if T > 1:
                 gate = self.smear_lambda.to(x.dtype) * torch.sigmoid(self.smear_gate(x[:, 1:, :24]))
                 x = torch.cat([x[:, :1], x[:, 1:] + gate * x[:, :-1]], dim=1)
             elif prev is not None:
                 gate = self.smear_lambda.to(x.dtype) * torch.sigmoid(self.smear_gate(x[:, :, :24]))
                 x = x + gate * prev
+            # this step's last (pre-smear) embedding for the next step; a buffer of the same shape is
+            # updated in place after its last read, so a graph-captured decode step stays correct
+            if prev is not None and prev.shape == last.shape and prev.dtype == last.dtype:
+                prev.copy_(last)
+            else:
+                kv_cache.prev_embedding = last
         x0 = x
         n_layer = self.config.n_layer
         backout_at = n_layer // 2

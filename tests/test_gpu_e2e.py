@@ -230,3 +230,17 @@ def test_fused_and_op_by_op_prologue_agree_in_the_model():
     assert torch.equal(runs[0][1].cache_seqlens, runs[1][1].cache_seqlens)
     dk = (runs[0][1].k_cache.float() - runs[1][1].k_cache.float()).abs().max()
     assert float(dk) <= 0.05
+
+
+@pytest.mark.parametrize("temperature", [0.0, 1.0])
+def test_graph_replayed_decode_steps_equal_eager_steps(temperature):
+    """Engine.generate with decode steps replayed from a HIP graph (no host sync in the fused-prologue
+    forward) produces exactly the eager loop's tokens: the graph is replayed every step with the
+    sampling and the tool-use state machine running eagerly in between."""
+    model = c1_model("perturbed").to(DEV)
+    runs = []
+    for use_graph in (False, True):
+        engine = Engine(model, SpecialTokens(), use_graph=use_graph)
+        runs.append([col for col, _ in engine.generate(GOLDEN["prompt"], num_samples=4, max_tokens=24,
+                                                       temperature=temperature, seed=7)])
+    assert runs[0] == runs[1]
