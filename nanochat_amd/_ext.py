@@ -138,16 +138,26 @@ def stream_handle(device: torch.device) -> int:
 # ---------------------------------------------------------------------------
 _workspaces: dict = {}
 _error_flags: dict = {}
+_retired: list = []  # outgrown workspaces, kept alive for graphs captured with them
 
 
 def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
+    """Split-K / prologue scratch for calls on `stream` (grows, never shrinks).
+
+    Buffers are created outside inference mode (they outlive the call that
+    made them), and a buffer that is outgrown is kept alive, not freed: a HIP
+    graph captured with it may still be replayed.
+    """
     if nbytes == 0:
         return None
     key = (device.index, stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
         cap = max(nbytes, 2 * buf.numel() if buf is not None else 0, 1 << 20)
-        buf = torch.empty(cap, dtype=torch.uint8, device=device)
+        if buf is not None:
+            _retired.append(buf)
+        with torch.inference_mode(False):
+            buf = torch.empty(cap, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf
 
@@ -155,7 +165,8 @@ def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | 
 def error_flag(device: torch.device) -> torch.Tensor:
     flag = _error_flags.get(device.index)
     if flag is None:
-        flag = torch.zeros(1, dtype=torch.int32, device=device)
+        with torch.inference_mode(False):
+            flag = torch.zeros(1, dtype=torch.int32, device=device)
         _error_flags[device.index] = flag
     return flag
 

@@ -49,10 +49,22 @@ def rms(x):
 
 
 class CastLinear(nn.Linear):
-    """Bias-free linear whose fp32 master weight is cast to the activation dtype."""
+    """Bias-free linear whose fp32 master weight is cast to the activation dtype.
+
+    Without autograd the cast is kept (keyed by dtype and the weight's version
+    counter) instead of being redone on every call: the same values, without
+    re-reading the fp32 weights each decode step.
+    """
 
     def forward(self, x):
-        return F.linear(x, self.weight.to(dtype=x.dtype))
+        if torch.is_grad_enabled() or self.weight.dtype == x.dtype:
+            return F.linear(x, self.weight.to(dtype=x.dtype))
+        key = (x.dtype, self.weight._version, self.weight.data_ptr())
+        cached = getattr(self, "_cast", None)
+        if cached is None or cached[0] != key:
+            cached = (key, self.weight.to(dtype=x.dtype))
+            self._cast = cached
+        return F.linear(x, cached[1])
 
 
 def carries_value_embedding(layer, n_layer):
