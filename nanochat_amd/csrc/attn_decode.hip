@@ -71,6 +71,11 @@ namespace nckv {
 namespace {
 
 constexpr int kWavesPerWG = NC_DECODE_WAVES;
+// Wide workgroups: 8 waves, for plans whose groups fit one workgroup per CU
+// and need no split (see plan_attention); their LDS merge arrays bound GB * D,
+// and GB <= 4 keeps every instantiation within 256 VGPRs.
+constexpr int kWideWaves = 8;
+constexpr int kWideMaxElems = 512;
 constexpr float kNegBig = -1.0e30f;   // finite "minus infinity" for running maxima
 constexpr int kMaxMergeSplits = 256;  // split cap of the launch plan
 constexpr int kXcds = 8;              // MI355X: workgroups go round-robin over 8 XCDs
@@ -324,14 +329,13 @@ void launch_merge_g(const DecodeParams& p, hipStream_t stream) {
   }
 }
 
-template <typename TC, bool QPK, int D, int GB>
-__global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const DecodeParams p) {
+template <typename TC, bool QPK, int D, int GB, int NW>
+__global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodeParams p) {
   constexpr int VEC = widen<TC>::N;
   constexpr int LPK = D / VEC;            // lanes per key row
   constexpr int KPI = kWave / LPK;        // keys per load instruction
   constexpr int NI = (GB >= 4) ? NC_DECODE_NI_GQA : NC_DECODE_NI;  // loads per tile (K and V each)
   constexpr int TILE = KPI * NI;          // keys per wave tile
-  constexpr int NW = kWavesPerWG;
   constexpr int EB = elem<TC>::kBytes;
   static_assert(LPK >= 1 && LPK <= kWave && KPI * LPK == kWave, "head_dim / dtype");
 
@@ -642,34 +646,47 @@ __global__ __launch_bounds__(kWavesPerWG * kWave) void decode_attn_kernel(const 
 
 
 template <typename TC, bool QPK, int D, int GB>
-hipError_t launch_g(const DecodeParams& p, int64_t n_wg, hipStream_t stream) {
-  hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB>), dim3(static_cast<unsigned>(n_wg)),
-                     dim3(kWavesPerWG * kWave), 0, stream, p);
+hipError_t launch_g(const DecodeParams& p, int64_t n_wg, bool wide, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(n_wg));
+  if constexpr (GB <= 4 && GB * D <= kWideMaxElems) {
+    if (wide) {
+      hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWideWaves>), grid, dim3(kWideWaves * kWave), 0,
+                         stream, p);
+      if (p.num_splits > 1) launch_merge_g<D, GB>(p, stream);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWavesPerWG>), grid, dim3(kWavesPerWG * kWave), 0, stream,
+                     p);
   if (p.num_splits > 1) launch_merge_g<D, GB>(p, stream);
   return hipGetLastError();
 }
 
 template <typename TC, bool QPK, int D>
-hipError_t launch_d(const DecodeParams& p, int gb, int64_t n_wg, hipStream_t stream) {
+hipError_t launch_d(const DecodeParams& p, int gb, int64_t n_wg, bool wide, hipStream_t stream) {
   switch (gb) {
-    case 8: return launch_g<TC, QPK, D, 8>(p, n_wg, stream);
-    case 4: return launch_g<TC, QPK, D, 4>(p, n_wg, stream);
-    case 2: return launch_g<TC, QPK, D, 2>(p, n_wg, stream);
-    default: return launch_g<TC, QPK, D, 1>(p, n_wg, stream);
+    case 8: return launch_g<TC, QPK, D, 8>(p, n_wg, wide, stream);
+    case 4: return launch_g<TC, QPK, D, 4>(p, n_wg, wide, stream);
+    case 2: return launch_g<TC, QPK, D, 2>(p, n_wg, wide, stream);
+    default: return launch_g<TC, QPK, D, 1>(p, n_wg, wide, stream);
   }
 }
 
 template <typename TC, bool QPK>
-hipError_t launch_dt(const DecodeParams& p, int64_t head_dim, int gb, int64_t n_wg, hipStream_t stream) {
+hipError_t launch_dt(const DecodeParams& p, int64_t head_dim, int gb, int64_t n_wg, bool wide, hipStream_t stream) {
   switch (head_dim) {
-    case 32: return launch_d<TC, QPK, 32>(p, gb, n_wg, stream);
-    case 64: return launch_d<TC, QPK, 64>(p, gb, n_wg, stream);
-    case 128: return launch_d<TC, QPK, 128>(p, gb, n_wg, stream);
-    default: return launch_d<TC, QPK, 256>(p, gb, n_wg, stream);
+    case 32: return launch_d<TC, QPK, 32>(p, gb, n_wg, wide, stream);
+    case 64: return launch_d<TC, QPK, 64>(p, gb, n_wg, wide, stream);
+    case 128: return launch_d<TC, QPK, 128>(p, gb, n_wg, wide, stream);
+    default: return launch_d<TC, QPK, 256>(p, gb, n_wg, wide, stream);
   }
 }
 
 }  // namespace
+
+bool decode_wide_supported(int head_block, int64_t head_dim) {
+  return head_block <= 4 && head_block * head_dim <= kWideMaxElems;
+}
 
 bool decode_supports(int cache_dtype, int64_t head_dim) {
   (void)cache_dtype;
@@ -781,13 +798,13 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
   const int gb = plan.head_block;
   switch (a.cache_dtype) {
     case NC_DTYPE_BF16:
-      return qpk ? launch_dt<bf16, true>(p, a.head_dim, gb, plan.n_wg, stream)
-                 : launch_dt<bf16, false>(p, a.head_dim, gb, plan.n_wg, stream);
+      return qpk ? launch_dt<bf16, true>(p, a.head_dim, gb, plan.n_wg, plan.wide, stream)
+                 : launch_dt<bf16, false>(p, a.head_dim, gb, plan.n_wg, plan.wide, stream);
     case NC_DTYPE_F16:
-      return qpk ? launch_dt<f16, true>(p, a.head_dim, gb, plan.n_wg, stream)
-                 : launch_dt<f16, false>(p, a.head_dim, gb, plan.n_wg, stream);
+      return qpk ? launch_dt<f16, true>(p, a.head_dim, gb, plan.n_wg, plan.wide, stream)
+                 : launch_dt<f16, false>(p, a.head_dim, gb, plan.n_wg, plan.wide, stream);
     default:
-      return launch_dt<float, false>(p, a.head_dim, gb, plan.n_wg, stream);
+      return launch_dt<float, false>(p, a.head_dim, gb, plan.n_wg, plan.wide, stream);
   }
 }
 

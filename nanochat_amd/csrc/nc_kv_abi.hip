@@ -21,6 +21,11 @@ constexpr int64_t kChunkMinTokens = 8;
 // 512-key splits; a 16k-key GQA chunk batch: 7.95 ms at 512, 10.8 unsplit).
 constexpr int64_t kChunkKeysPerSplit = 512;
 constexpr int64_t kChunkSplitAbove = 2048;
+// Decode with wide workgroups and no split: at most this many groups (one per
+// CU) and this many keys per row.
+constexpr int64_t kWideMinGroups = 128;
+constexpr int64_t kWideMaxGroups = 256;
+constexpr int64_t kWideMaxKeys = 4096;
 
 bool valid_dtype(int d) { return d == NC_DTYPE_F32 || d == NC_DTYPE_F16 || d == NC_DTYPE_BF16; }
 int64_t dtype_bytes(int d) { return d == NC_DTYPE_F32 ? 4 : 2; }
@@ -66,6 +71,19 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   if (ns > cap) {
     kps = ((max_keys + cap - 1) / cap + 63) / 64 * 64;
     ns = (max_keys + kps - 1) / kps;
+  }
+  // Between half and one chip's worth of groups with short rows: one 8-wave
+  // workgroup per group streams the whole row (no split, so no merge launch).
+  // Measured on MI355X: d24 decode (192 groups x 513-1153 keys) 0.469 -> 0.391
+  // ms/step; fewer groups leave CUs idle (d26 SSSL decode, 104 groups x
+  // 1025-3328 keys: 0.562 -> 0.606), so they keep the split plan.
+  plan->wide = false;
+  if (a.t_new == 1 && a.keys_per_split == 0 && plan->n_groups >= kWideMinGroups && plan->n_groups <= kWideMaxGroups &&
+      max_keys <= kWideMaxKeys &&
+      decode_wide_supported(hb, a.head_dim)) {
+    plan->wide = true;
+    kps = (max_keys + 63) / 64 * 64;
+    ns = 1;
   }
   plan->keys_per_split = static_cast<int>(kps);
   plan->num_splits = static_cast<int>(ns);

@@ -25,6 +25,7 @@ struct AttnPlan {
   int keys_per_split;
   int num_splits;
   int64_t n_wg;        // decode grid size
+  bool wide;           // decode with 8-wave workgroups and one split (few groups, short rows)
   bool use_chunk;      // T_new > 1 on the MFMA chunk kernel
   int chunk_keys_per_split;
   int chunk_splits;    // > 1: chunk partials merged by the split-merge kernel
@@ -44,6 +45,7 @@ hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const Attn
 hipError_t launch_rope_append(const nc_attn_args& a, const nc_qk_prologue& pro, void* q_out, hipStream_t stream);
 
 bool decode_supports(int cache_dtype, int64_t head_dim);
+bool decode_wide_supported(int head_block, int64_t head_dim);
 bool chunk_supports(const nc_attn_args& a);
 hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream);
 int chunk_rows_per_wg();

@@ -295,3 +295,14 @@ def test_decode_merge_beyond_16_splits(H, H_kv, kps):
     """Rows of 40+ splits take the 32-slot merge (float4 per thread), short rows in the same call
     write directly or merge a few slots."""
     _check(230 + H, 3, 1, H, H_kv, 128, 5200, [5000, 70, 2100], -1, kps=kps)
+
+
+@pytest.mark.parametrize("B,H,H_kv,D,seqlens,window", [
+    (16, 12, 12, 128, [1024] * 16, 512),            # C3 decode shape, S layer (8-wave workgroups, no split)
+    (12, 13, 13, 128, [3072, 3000, 2999, 3072, 1, 0, 3100, 3071, 4095, 2, 64, 65], -1),  # ragged, up to 4096 keys
+    (40, 16, 4, 128, [(i * 977) % 4000 for i in range(40)], -1),  # GQA 4:1 head blocks, 160 groups
+    (20, 8, 8, 256, [(i * 613) % 4090 for i in range(20)], 700),  # head_dim 256, window
+])
+def test_decode_wide_workgroups_no_split(B, H, H_kv, D, seqlens, window):
+    """128..256 groups with rows <= 4096 keys take 8-wave workgroups with one split (no merge launch)."""
+    _check(240 + B, B, 1, H, H_kv, D, max(seqlens) + 4, seqlens, window)
