@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NC_KV_ABI_VERSION 2
+#define NC_KV_ABI_VERSION 3
 
 /* Element types (the torch dtypes the reference path uses). */
 enum nc_dtype {
@@ -113,9 +113,14 @@ int nc_kv_fanout(const nc_fanout_args* args, void* stream);
  * is fp32.  The fused path (t_new == 1) appends and attends in one launch;
  * t_new > 1 appends first and then attends (two launches, same stream).
  * When a row's keys span several splits, partial results go to the workspace
- * (nc_attn_workspace_bytes; 0 bytes when every row fits one split) and a
- * second small kernel merges them.  The workspace needs no initialisation;
- * calls sharing a workspace must not overlap in time (use one per stream).
+ * (nc_attn_workspace_bytes; 0 bytes when every row fits one split) and are
+ * merged by the last split of each (row, query, head block) in the same
+ * launch, or by a second small kernel (chunk splits; more than
+ * NC_WORKSPACE_SYNC_BYTES / 4 groups).  A non-empty workspace begins with
+ * NC_WORKSPACE_SYNC_BYTES of split counters: they must be zero before the
+ * buffer's first use (e.g. allocate it zeroed), and every call leaves them
+ * zero; the rest needs no initialisation.  Calls sharing a workspace must not
+ * overlap in time (use one per stream).
  * ------------------------------------------------------------------------- */
 typedef struct nc_attn_args {
   const void* q;                 /* (B, T_new, H, D) */
@@ -142,6 +147,10 @@ typedef struct nc_attn_args {
   int32_t keys_per_split;        /* keys one workgroup covers before a split-K merge;
                                     0: library default; else a multiple of 64 */
 } nc_attn_args;
+
+/* Leading bytes of every non-empty workspace that hold split counters
+ * (zero before first use, left zero by every call). */
+#define NC_WORKSPACE_SYNC_BYTES 65536
 
 /* Bytes of workspace nc_attn_kvcache needs for these arguments. */
 size_t nc_attn_workspace_bytes(const nc_attn_args* args);

@@ -16,12 +16,14 @@ import torch
 # NANOCHAT_AMD_LIB points at another build of the same library (e.g. a tuning
 # variant); by default the in-tree build next to this file is loaded.
 LIB_PATH = Path(os.environ.get("NANOCHAT_AMD_LIB", Path(__file__).resolve().parent / "libnc_kv.so"))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 NC_DEVERR_OVERFLOW = 1
 NC_DEVERR_ROPE_RANGE = 2
+# leading workspace bytes holding split counters: zero before first use, left zero by every call
+NC_WORKSPACE_SYNC_BYTES = 65536
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -144,9 +146,11 @@ _retired: list = []  # outgrown workspaces, kept alive for graphs captured with 
 def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
     """Split-K / prologue scratch for calls on `stream` (grows, never shrinks).
 
-    Buffers are created outside inference mode (they outlive the call that
-    made them), and a buffer that is outgrown is kept alive, not freed: a HIP
-    graph captured with it may still be replayed.
+    Buffers are allocated zeroed (their first NC_WORKSPACE_SYNC_BYTES hold the
+    split counters, which the library keeps at zero between calls) and outside
+    inference mode (they outlive the call that made them).  A buffer that is
+    outgrown is kept alive, not freed: a HIP graph captured with it may still
+    be replayed.
     """
     if nbytes == 0:
         return None
@@ -157,7 +161,7 @@ def workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | 
         if buf is not None:
             _retired.append(buf)
         with torch.inference_mode(False):
-            buf = torch.empty(cap, dtype=torch.uint8, device=device)
+            buf = torch.zeros(cap, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf
 

@@ -19,14 +19,22 @@
 // Split merge: a query whose key range fits one split (always, when the plan
 // has one split) gets its output from the decode kernel directly.  Otherwise
 // each of its splits writes (o, m, l) partials to the workspace (a split past
-// the end of the range does nothing) and merge_splits_kernel, the next launch
-// on the stream, recomputes the query's split count from cache_seqlens and
-// combines exactly those slots with the log-sum-exp rule.  The
-// kernel boundary is the only synchronisation: an in-kernel "last split
-// merges" scheme needs agent-scope release fences (L2 write-back), which
-// measured 3-10x slower on MI355X.  The splits of one (b, t, unit) run on the
-// XCD of its merge block (workgroups are dispatched round-robin over the 8
-// XCDs), so the merge reads the partials from the L2 they were written to.
+// the end of the range does nothing) and the partials are combined with the
+// log-sum-exp rule, in one of two ways:
+//  - in-kernel (the plan passes `tickets`): partials are written with
+//    agent-coherent stores (sc1: written through the XCD's L2), each thread
+//    waits for its stores to complete (vmcnt(0)), then the workgroup takes a
+//    ticket with an agent-scope atomic add.  The split that draws the last
+//    ticket reads the slots back with agent-coherent loads, merges them and
+//    resets the ticket to zero.  No L2 write-back or invalidate (the
+//    release/acquire fences, buffer_wbl2 / buffer_inv, which measured 3-10x
+//    slower on MI355X) and no waiting on other workgroups: the last arrival
+//    finds every partial complete.
+//  - merge_splits_kernel, the next launch on the stream (chunk splits, and
+//    decode plans with more groups than tickets): it recomputes the query's
+//    split count from cache_seqlens and combines exactly those slots.
+// The splits of one (b, t, unit) run on one XCD (workgroups are dispatched
+// round-robin over the 8 XCDs), next to each other in launch order.
 //
 // Fused append (t_new == 1 with k/v given): the split owning position s_b
 // takes the new key/value from the k/v inputs (converted to the cache dtype,
@@ -91,6 +99,7 @@ struct DecodeParams {
   int32_t* err;
   float* part_ml;
   float* part_o;
+  uint32_t* tickets;  // non-null: splits merge in-kernel (one zeroed counter per group)
   int64_t q_sb, q_st, q_sh;
   int64_t kc_sb, kc_st, kc_sh;
   int64_t vc_sb, vc_st, vc_sh;
@@ -329,6 +338,21 @@ void launch_merge_g(const DecodeParams& p, hipStream_t stream) {
   }
 }
 
+// Agent-coherent accesses for the in-kernel split merge: relaxed agent-scope
+// atomics compile to plain vector loads/stores with the sc1 bit (coherent
+// across the XCDs' L2s), without the L2 write-back / invalidate that a
+// release / acquire fence adds.
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float coherent_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// slots folded per round trip by the in-kernel merge (the default split
+// gives at most 8 slots per row at 2048 keys)
+constexpr int kInKernelMergeChunk = 8;
+
 template <typename TC, bool QPK, int D, int GB, int NW>
 __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodeParams p) {
   constexpr int VEC = widen<TC>::N;
@@ -344,6 +368,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   __shared__ float sm_l[NW][GB];
   __shared__ float sm_w[NW][GB];
   __shared__ float sm_L[GB];
+  __shared__ int sm_last;  // this split drew the group's last ticket: it merges
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -631,16 +656,81 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     }
     return;
   }
+  if (p.tickets == nullptr) {  // merge_splits_kernel combines the partials
+    for (int idx = tid; idx < GB * D; idx += NW * kWave) {
+      const int g = idx / D, d = idx % D;
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) acc += sm_o[w][g][d] * sm_w[w][g];
+      p.part_o[((pair0 + g) * p.num_splits + split) * D + d] = acc;
+    }
+    if (tid < GB) {
+      *reinterpret_cast<float2*>(p.part_ml + ((pair0 + tid) * p.num_splits + split) * 2) =
+          make_float2(sm_m[0][tid], sm_L[tid]);
+    }
+    return;
+  }
+
+  // ---- in-kernel merge: publish the partial, take a ticket, the last split merges ----
   for (int idx = tid; idx < GB * D; idx += NW * kWave) {
     const int g = idx / D, d = idx % D;
     float acc = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) acc += sm_o[w][g][d] * sm_w[w][g];
-    p.part_o[((pair0 + g) * p.num_splits + split) * D + d] = acc;
+    coherent_store(p.part_o + ((pair0 + g) * p.num_splits + split) * D + d, acc);
   }
   if (tid < GB) {
-    *reinterpret_cast<float2*>(p.part_ml + ((pair0 + tid) * p.num_splits + split) * 2) =
-        make_float2(sm_m[0][tid], sm_L[tid]);
+    float* ml = p.part_ml + ((pair0 + tid) * p.num_splits + split) * 2;
+    coherent_store(ml, sm_m[0][tid]);
+    coherent_store(ml + 1, sm_L[tid]);
+  }
+  // every thread's partial stores have completed (reached the agent's point
+  // of coherence) before the barrier, hence before the ticket is taken
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t tk = __hip_atomic_fetch_add(p.tickets + group, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = tk + 1 == static_cast<uint32_t>(kr.nsplit);
+    // every split of this group has drawn its ticket: back to zero for the next call
+    if (last) __hip_atomic_store(p.tickets + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm_last = last;
+  }
+  __syncthreads();
+  if (!sm_last) return;
+  __asm__ volatile("" ::: "memory");
+  const int nsplit = kr.nsplit;
+  for (int idx = tid; idx < GB * D; idx += NW * kWave) {
+    const int g = idx / D, d = idx % D;
+    const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
+    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d;
+    float M = kNegBig, L = 0.0f, O = 0.0f;
+    for (int sp0 = 0; sp0 < nsplit; sp0 += kInKernelMergeChunk) {
+      float ms[kInKernelMergeChunk], ls[kInKernelMergeChunk], os[kInKernelMergeChunk];
+#pragma unroll
+      for (int u = 0; u < kInKernelMergeChunk; ++u) {
+        const int sp = sp0 + u;
+        const bool in = sp < nsplit;
+        ms[u] = in ? coherent_load(ml + 2 * sp) : kNegBig;
+        ls[u] = in ? coherent_load(ml + 2 * sp + 1) : 0.0f;
+        os[u] = in ? coherent_load(po + static_cast<int64_t>(sp) * D) : 0.0f;
+      }
+      float mx = M;
+#pragma unroll
+      for (int u = 0; u < kInKernelMergeChunk; ++u) mx = ls[u] > 0.0f ? fmaxf(mx, ms[u]) : mx;
+      const float a = fast_exp2(M - mx);
+      L *= a;
+      O *= a;
+#pragma unroll
+      for (int u = 0; u < kInKernelMergeChunk; ++u) {
+        const bool live = ls[u] > 0.0f;
+        const float w = live ? fast_exp2(ms[u] - mx) : 0.0f;
+        L = __builtin_fmaf(ls[u], w, L);
+        O = live ? __builtin_fmaf(os[u], w, O) : O;
+      }
+      M = mx;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    store_any(p.out, (pair0 + g) * D + d, p.q_dtype, O * inv);
   }
 }
 
@@ -652,13 +742,13 @@ hipError_t launch_g(const DecodeParams& p, int64_t n_wg, bool wide, hipStream_t 
     if (wide) {
       hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWideWaves>), grid, dim3(kWideWaves * kWave), 0,
                          stream, p);
-      if (p.num_splits > 1) launch_merge_g<D, GB>(p, stream);
+      if (p.num_splits > 1 && p.tickets == nullptr) launch_merge_g<D, GB>(p, stream);
       return hipGetLastError();
     }
   }
   hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWavesPerWG>), grid, dim3(kWavesPerWG * kWave), 0, stream,
                      p);
-  if (p.num_splits > 1) launch_merge_g<D, GB>(p, stream);
+  if (p.num_splits > 1 && p.tickets == nullptr) launch_merge_g<D, GB>(p, stream);
   return hipGetLastError();
 }
 
@@ -723,6 +813,7 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.k_new = a.k; p.v_new = a.v;
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
   p.part_ml = s.part_ml; p.part_o = s.part_o;
+  p.tickets = plan.merge_in_kernel ? s.tickets : nullptr;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
@@ -770,6 +861,7 @@ hipError_t launch_merge_d(const DecodeParams& p, int gb, hipStream_t stream) {
 hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
                               hipStream_t stream) {
   DecodeParams p = make_params(a, plan, s, false);
+  p.tickets = nullptr;
   p.num_splits = plan.chunk_splits;
   p.keys_per_split = plan.chunk_keys_per_split;
   p.merge_qb = chunk_rows_per_wg() / plan.head_block;

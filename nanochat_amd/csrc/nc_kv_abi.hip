@@ -26,6 +26,20 @@ constexpr int64_t kChunkSplitAbove = 2048;
 constexpr int64_t kWideMinGroups = 128;
 constexpr int64_t kWideMaxGroups = 256;
 constexpr int64_t kWideMaxKeys = 4096;
+// Decode splits merged by their last workgroup (one uint32 ticket per group at
+// the start of every non-empty workspace) instead of a merge launch, for grids
+// of at most kMergeInKernelMaxWG workgroups.  Each workgroup then ends with a
+// ticket round trip while holding its CU slot, which costs more than the
+// merge launch once there are many workgroups per CU.  Measured on MI355X
+// (us per call, merge launch -> in-kernel): d26 S layers (104 groups x 5
+// splits) 15.3 -> 13.8; B=1 at 32k keys (10 x 129) 58.3 -> 52.5; d20 B=32
+// at 1088 keys (320 x 5) 34.5 -> 33.7; but C2 (320 x 9) 39.5 -> 40.3 and
+// B=32 at 4k keys (320 x 17) 108.4 -> 113.
+#ifndef NC_DECODE_MERGE_IN_KERNEL
+#define NC_DECODE_MERGE_IN_KERNEL 1  // 0: decode splits always use the merge launch
+#endif
+constexpr int64_t kMaxTickets = NC_WORKSPACE_SYNC_BYTES / 4;
+constexpr int64_t kMergeInKernelMaxWG = NC_DECODE_MERGE_IN_KERNEL ? 2048 : 0;
 
 bool valid_dtype(int d) { return d == NC_DTYPE_F32 || d == NC_DTYPE_F16 || d == NC_DTYPE_BF16; }
 int64_t dtype_bytes(int d) { return d == NC_DTYPE_F32 ? 4 : 2; }
@@ -111,6 +125,9 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
     if (cgroups * ((a.t_new + qb - 1) / qb) * cns > INT32_MAX) return NC_ERR_BAD_SHAPE;
   }
   const int64_t merge_splits = plan->use_chunk ? plan->chunk_splits : ns;
+  // decode splits: the last workgroup of each group merges (no merge launch)
+  plan->merge_in_kernel = !plan->use_chunk && ns > 1 && plan->n_groups <= kMaxTickets &&
+                          plan->n_groups * ns <= kMergeInKernelMaxWG;
   if (merge_splits > 1) {
     const size_t pairs = static_cast<size_t>(a.batch * a.t_new * a.n_heads);
     plan->ml_bytes = round256(pairs * merge_splits * 2 * 4);
@@ -118,7 +135,9 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   } else {
     plan->ml_bytes = plan->o_bytes = 0;
   }
-  plan->total_bytes = plan->ml_bytes + plan->o_bytes;
+  // every non-empty workspace starts with the sync region, whether or not
+  // this call uses it, so no call's scratch ever lands on the counters
+  plan->total_bytes = plan->ml_bytes + plan->o_bytes > 0 ? NC_WORKSPACE_SYNC_BYTES + plan->ml_bytes + plan->o_bytes : 0;
   return NC_OK;
 }
 
@@ -226,8 +245,9 @@ int check_attention(const nc_attn_args& a, AttnPlan* plan) {
 AttnScratch carve(const nc_attn_args& a, const AttnPlan& plan) {
   AttnScratch s;
   char* ws = static_cast<char*>(a.workspace);
-  s.part_ml = reinterpret_cast<float*>(ws);
-  s.part_o = reinterpret_cast<float*>(ws + plan.ml_bytes);
+  s.tickets = reinterpret_cast<uint32_t*>(ws);
+  s.part_ml = reinterpret_cast<float*>(ws + NC_WORKSPACE_SYNC_BYTES);
+  s.part_o = reinterpret_cast<float*>(ws + NC_WORKSPACE_SYNC_BYTES + plan.ml_bytes);
   return s;
 }
 
@@ -269,6 +289,15 @@ size_t rope_q_bytes(const nc_attn_args& a) {
                   static_cast<size_t>(dtype_bytes(a.q_dtype)));
 }
 
+// Workspace offset of the prologue's q (after the sync region and partials).
+size_t rope_q_offset(const AttnPlan& plan) { return NC_WORKSPACE_SYNC_BYTES + plan.ml_bytes + plan.o_bytes; }
+
+// Workspace bytes of nc_attn_kvcache_rope.
+size_t rope_need(const nc_attn_args& a, const AttnPlan& plan) {
+  const size_t q = rope_q_bytes(a);
+  return q > 0 ? rope_q_offset(plan) + q : plan.total_bytes;
+}
+
 }  // namespace
 
 int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
@@ -288,7 +317,7 @@ size_t nc_attn_rope_workspace_bytes(const nc_attn_args* args) {
   if (args == nullptr) return 0;
   AttnPlan plan;
   if (plan_attention(*args, &plan) != NC_OK) return 0;
-  return plan.total_bytes + rope_q_bytes(*args);
+  return rope_need(*args, plan);
 }
 
 int nc_attn_kvcache_rope(const nc_attn_args* args, const nc_qk_prologue* prologue, void* stream) {
@@ -305,7 +334,7 @@ int nc_attn_kvcache_rope(const nc_attn_args* args, const nc_qk_prologue* prologu
   AttnPlan plan;
   const int st = check_attention(a, &plan);
   if (st != NC_OK) return st;
-  const size_t need = plan.total_bytes + rope_q_bytes(a);
+  const size_t need = rope_need(a, plan);
   if (need > 0 && (a.workspace == nullptr || a.workspace_bytes < need || !aligned16(a.workspace))) {
     return NC_ERR_WORKSPACE;
   }
@@ -315,7 +344,7 @@ int nc_attn_kvcache_rope(const nc_attn_args* args, const nc_qk_prologue* prologu
   const AttnScratch s = carve(a, plan);
   if (a.t_new == 1) return run_attention(a, plan, s, &pro, hs);
   // t_new > 1: prologue kernel (q -> workspace, k/v -> cache), then attention without append
-  void* q_out = static_cast<char*>(a.workspace) + plan.total_bytes;
+  void* q_out = static_cast<char*>(a.workspace) + rope_q_offset(plan);
   if (launch_rope_append(a, pro, q_out, hs) != hipSuccess) return NC_ERR_LAUNCH;
   nc_attn_args b = a;
   b.q = q_out;

@@ -13,6 +13,7 @@ namespace nckv {
 struct AttnScratch {
   float* part_ml;      // (pair, split, 2): running max (log2 domain) and sum
   float* part_o;       // (pair, split, D): unnormalised output
+  uint32_t* tickets;   // (group,): split arrival counters, zero between calls
 };
 
 // Launch plan shared by nc_attn_workspace_bytes and nc_attn_kvcache.
@@ -26,6 +27,7 @@ struct AttnPlan {
   int num_splits;
   int64_t n_wg;        // decode grid size
   bool wide;           // decode with 8-wave workgroups and one split (few groups, short rows)
+  bool merge_in_kernel;  // decode splits merged by their last workgroup (tickets), no merge launch
   bool use_chunk;      // T_new > 1 on the MFMA chunk kernel
   int chunk_keys_per_split;
   int chunk_splits;    // > 1: chunk partials merged by the split-merge kernel

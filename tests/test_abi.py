@@ -30,6 +30,14 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.nc_abi_version() == _ext.ABI_VERSION
 
 
+def test_header_constants_match_python_mirror():
+    text = HEADER.read_text()
+    for name in ("NC_KV_ABI_VERSION", "NC_WORKSPACE_SYNC_BYTES", "NC_DEVERR_OVERFLOW", "NC_DEVERR_ROPE_RANGE"):
+        value = int(re.search(r"#define %s (\d+)" % name, text).group(1))
+        py = _ext.ABI_VERSION if name == "NC_KV_ABI_VERSION" else getattr(_ext, name)
+        assert py == value, name
+
+
 def test_struct_layouts_match_header_field_order():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     for cname, pystruct in (("nc_append_args", _ext.AppendArgs), ("nc_fanout_args", _ext.FanoutArgs),
@@ -74,7 +82,7 @@ def test_workspace_plan_for_d20_decode():
     # 64 KiB of K per head per split -> 256 keys; 2304 / 256 = 9 splits;
     # (m, l) and o partials per (row, head, split)
     pairs = 32 * 10
-    expect = 256 * ((pairs * 9 * 8 + 255) // 256) + pairs * 9 * 128 * 4
+    expect = _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((pairs * 9 * 8 + 255) // 256) + pairs * 9 * 128 * 4
     assert lib.nc_attn_workspace_bytes(ctypes.byref(a)) == expect
 
 
@@ -85,7 +93,7 @@ def test_workspace_zero_for_single_split_and_window_caps_keys():
     assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=4096, window=256))) > 0
     # split cap: 65536 keys at the 256-key default is exactly 256 splits; 80000 keys widen the split
     assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(B=1, H=1, H_kv=1, T_max=80000))) == \
-        256 * ((1 * 250 * 8 + 255) // 256) + 250 * 128 * 4
+        _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((1 * 250 * 8 + 255) // 256) + 250 * 128 * 4
 
 
 def test_invalid_arguments_are_rejected_before_launch():

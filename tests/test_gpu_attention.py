@@ -306,3 +306,39 @@ def test_decode_merge_beyond_16_splits(H, H_kv, kps):
 def test_decode_wide_workgroups_no_split(B, H, H_kv, D, seqlens, window):
     """128..256 groups with rows <= 4096 keys take 8-wave workgroups with one split (no merge launch)."""
     _check(240 + B, B, 1, H, H_kv, D, max(seqlens) + 4, seqlens, window)
+
+
+def _sync_region_is_zero():
+    """Every stream workspace's leading split counters are back at zero."""
+    torch.cuda.synchronize()
+    for buf in list(_ext._workspaces.values()):
+        head = buf[:_ext.NC_WORKSPACE_SYNC_BYTES]
+        assert int(head.count_nonzero()) == 0
+
+
+def test_decode_in_kernel_merge_counters_return_to_zero():
+    """Split merges by the last workgroup of each group: calls whose split
+    counts per row change from call to call (ragged rows, 64-key splits, more
+    than 8 slots per row), a chunk call in between, and the counters are zero
+    after each call."""
+    cases = [
+        (4, 8, 8, [3000, 7, 64, 65]),           # up to 47 splits: several merge rounds
+        (6, 16, 4, [1, 640, 2999, 128, 129, 0]),
+        (2, 4, 4, [2500, 2501]),
+    ]
+    for i, (B, H, H_kv, seqlens) in enumerate(cases):
+        _check(300 + i, B, 1, H, H_kv, 128, 3072, seqlens, -1, kps=64)
+        _sync_region_is_zero()
+        _check(310 + i, B, 16, H, H_kv, 128, 3072, [min(s, 3000) for s in seqlens], -1)  # chunk partials
+        _sync_region_is_zero()
+        _check(320 + i, B, 1, H, H_kv, 128, 3072, [max(s - 1, 0) for s in seqlens], 700, kps=128)
+        _sync_region_is_zero()
+
+
+def test_decode_more_groups_than_counters_uses_merge_launch():
+    """16640 (row, head) groups exceed the 16384 counters of the sync region:
+    the plan falls back to the merge kernel; same results."""
+    B, H = 65, 256
+    seqlens = [(b * 37) % 200 for b in range(B)]
+    _check(330, B, 1, H, H, 32, 200, seqlens, -1, kps=64)
+    _sync_region_is_zero()
