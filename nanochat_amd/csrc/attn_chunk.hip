@@ -41,6 +41,7 @@
 // loaded into registers while the current one is consumed from LDS.
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "nc_kv_common.hpp"
 #include "nc_kv_internal.hpp"
@@ -102,6 +103,13 @@ template <> struct mfma_t<bf16> {
     c = make_float4(acc[0], acc[1], acc[2], acc[3]);
   }
   __device__ __forceinline__ static uint16_t from_float(float x) { return f32_to_bf16_rne(x); }
+  // two values rounded to nearest even, packed (v_cvt_pk_bf16_f32)
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 h2 __attribute__((ext_vector_type(2)));
+    const f2 x = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
+  }
 };
 template <> struct mfma_t<f16> {
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
@@ -112,6 +120,12 @@ template <> struct mfma_t<f16> {
     c = make_float4(acc[0], acc[1], acc[2], acc[3]);
   }
   __device__ __forceinline__ static uint16_t from_float(float x) { return f32_to_f16_rne(x); }
+  __device__ __forceinline__ static uint32_t pack2(float a, float b) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const f2 x = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
+  }
 };
 
 template <typename TC, int D, int GB>
@@ -213,38 +227,66 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
 
   // ---- key tiles: registers hold the next tile while the current one is
   // consumed from LDS (a second register stage measured no faster) ----
+  // Thread chunk u of a tile is key key0 + u * KSTEP, 16-byte column dc0 (the
+  // plan keeps a tile's byte span below 2^31, so offsets are 32-bit).
+  constexpr int CPR = D / 8;                          // 16-byte chunks per key row
+  constexpr int KSTEP = kChunkWaves * kWave / CPR;    // keys between a thread's chunks
+  const int key0 = tid / CPR, dc0 = tid % CPR;
+  uint32_t koff[PER_THREAD], voff[PER_THREAD];
+#pragma unroll
+  for (int u = 0; u < PER_THREAD; ++u) {
+    koff[u] = static_cast<uint32_t>((key0 + u * KSTEP) * kst + dc0 * 16);
+    voff[u] = static_cast<uint32_t>((key0 + u * KSTEP) * vst + dc0 * 16);
+  }
   uint4 kreg[PER_THREAD], vreg[PER_THREAD];
   auto load_regs = [&](int kt0, uint4 (&kr)[PER_THREAD], uint4 (&vr)[PER_THREAD]) {
+    if (kt0 + kBN <= hi && kt0 + kBN <= new_lo) {
+      // whole tile inside the span and in the cache: no per-chunk checks
+      const char* kt = kbase + kt0 * kst;
+      const char* vt = vbase + kt0 * vst;
+#pragma unroll
+      for (int u = 0; u < PER_THREAD; ++u) {
+        kr[u] = *reinterpret_cast<const uint4*>(kt + koff[u]);
+        vr[u] = *reinterpret_cast<const uint4*>(vt + voff[u]);
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < PER_THREAD; ++u) {
-      const int c = tid + u * kChunkWaves * kWave;
-      const int j = kt0 + c / (D / 8);
-      const int dc = c % (D / 8);
+      const int j = kt0 + key0 + u * KSTEP;
       if (j < hi) {
         const bool from_new = j >= new_lo;
         const char* kp = from_new ? knew + (j - s) * knst : kbase + j * kst;
         const char* vp = from_new ? vnew + (j - s) * vnst : vbase + j * vst;
-        kr[u] = *reinterpret_cast<const uint4*>(kp + dc * 16);
-        vr[u] = *reinterpret_cast<const uint4*>(vp + dc * 16);
+        kr[u] = *reinterpret_cast<const uint4*>(kp + dc0 * 16);
+        vr[u] = *reinterpret_cast<const uint4*>(vp + dc0 * 16);
       } else {
         kr[u] = make_uint4(0, 0, 0, 0);
         vr[u] = make_uint4(0, 0, 0, 0);
       }
     }
   };
+  // wave-uniform bounds of this wave's query rows: tiles wholly inside every
+  // row's mask skip the per-element mask
+  const int qi_first = q0 + (wave * 16) / GB, qi_last = q0 + (wave * 16 + 15) / GB;
+  const bool wave_rows_full = qi_last < p.t_new;
+  const int qpos_first = s + qi_first, qpos_last = s + qi_last;
   auto tile_step = [&](int kt0, uint4 (&kr)[PER_THREAD], uint4 (&vr)[PER_THREAD]) {
     __syncthreads();  // previous tile's LDS reads are done
 #pragma unroll
     for (int u = 0; u < PER_THREAD; ++u) {
-      const int c = tid + u * kChunkWaves * kWave;
-      const int key = c / (D / 8);
-      const int dc = c % (D / 8);
-      *reinterpret_cast<uint4*>(ks + key * KROW + dc * 16) = kr[u];
-      *reinterpret_cast<uint4*>(vs + key * VROW + dc * 16) = vr[u];
-      const int j = kt0 + key;
-      if (j >= own_lo && j < hi) {
-        *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + j * kst + dc * 16) = kr[u];
-        *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + j * vst + dc * 16) = vr[u];
+      const int key = key0 + u * KSTEP;
+      *reinterpret_cast<uint4*>(ks + key * KROW + dc0 * 16) = kr[u];
+      *reinterpret_cast<uint4*>(vs + key * VROW + dc0 * 16) = vr[u];
+    }
+    if (kt0 + kBN > own_lo) {  // the tile holds new tokens this workgroup stores
+#pragma unroll
+      for (int u = 0; u < PER_THREAD; ++u) {
+        const int j = kt0 + key0 + u * KSTEP;
+        if (j >= own_lo && j < hi) {
+          *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + j * kst + dc0 * 16) = kr[u];
+          *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + j * vst + dc0 * 16) = vr[u];
+        }
       }
     }
     __syncthreads();
@@ -263,6 +305,8 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     }
 
     // ---- mask, scale, online softmax (each lane: one query row) ----
+    const bool interior = wave_rows_full && kt0 + kBN <= hi && kt0 + kBN - 1 <= qpos_first &&
+                          (p.window < 0 || kt0 >= qpos_last - p.window);
     float sv[4][4];
     float mt = -__builtin_inff();
 #pragma unroll
@@ -270,9 +314,12 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
       const float a4[4] = {acc_s[kb].x, acc_s[kb].y, acc_s[kb].z, acc_s[kb].w};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int j = kt0 + 16 * kb + 4 * lq + r;
-        const bool ok = row_ok && j >= row_lo && j <= qpos && j < hi;
-        sv[kb][r] = ok ? a4[r] * p.scale_log2 : -__builtin_inff();
+        sv[kb][r] = a4[r] * p.scale_log2;
+        if (!interior) {
+          const int j = kt0 + 16 * kb + 4 * lq + r;
+          const bool ok = row_ok && j >= row_lo && j <= qpos && j < hi;
+          sv[kb][r] = ok ? sv[kb][r] : -__builtin_inff();
+        }
         mt = fmaxf(mt, sv[kb][r]);
       }
     }
@@ -284,24 +331,26 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     uint32_t pk[4][2];  // P packed in the cache dtype: [key block][pair of r]
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      uint16_t ph[4];
+      float pv[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pv = fast_exp2(sv[kb][r] - m_new);
-        rs += pv;
-        ph[r] = mfma_t<TC>::from_float(pv);
+        pv[r] = fast_exp2(sv[kb][r] - m_new);
+        rs += pv[r];
       }
-      pk[kb][0] = static_cast<uint32_t>(ph[0]) | (static_cast<uint32_t>(ph[1]) << 16);
-      pk[kb][1] = static_cast<uint32_t>(ph[2]) | (static_cast<uint32_t>(ph[3]) << 16);
+      pk[kb][0] = mfma_t<TC>::pack2(pv[0], pv[1]);
+      pk[kb][1] = mfma_t<TC>::pack2(pv[2], pv[3]);
     }
     rs += __shfl_xor(rs, 16, kWave);
     rs += __shfl_xor(rs, 32, kWave);
     l_run = l_run * alpha + rs;
-    m_run = m_new;
+    // rescale the output only when some row's running max moved
+    if (__any(m_new != m_run)) {
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      acc_o[db].x *= alpha; acc_o[db].y *= alpha; acc_o[db].z *= alpha; acc_o[db].w *= alpha;
+      for (int db = 0; db < DB; ++db) {
+        acc_o[db].x *= alpha; acc_o[db].y *= alpha; acc_o[db].z *= alpha; acc_o[db].w *= alpha;
+      }
     }
+    m_run = m_new;
 
     // ---- O^T += V^T . P^T over the two 32-key chunks ----
 #pragma unroll
@@ -363,9 +412,11 @@ hipError_t launch_c(const ChunkParams& p, int gb, hipStream_t stream) {
 }  // namespace
 
 bool chunk_supports(const nc_attn_args& a) {
+  // a key tile's byte span (64 cache rows) must fit the kernel's 32-bit offsets
+  const int64_t tile_bytes = kBN * std::max(std::abs(a.kc_stride_t), std::abs(a.vc_stride_t)) * 2;
   return a.t_new > 1 && a.q_dtype == a.cache_dtype &&
          (a.cache_dtype == NC_DTYPE_BF16 || a.cache_dtype == NC_DTYPE_F16) &&
-         (a.head_dim == 64 || a.head_dim == 128);
+         (a.head_dim == 64 || a.head_dim == 128) && tile_bytes < (int64_t(1) << 31);
 }
 
 int chunk_rows_per_wg() { return kRows; }
