@@ -14,12 +14,17 @@ namespace {
 
 // Chunks of at least this many new tokens run on the MFMA chunk kernel.
 constexpr int64_t kChunkMinTokens = 8;
-// Default key span of one chunk-kernel split (8 tiles of 64 keys), used when
-// a workgroup's span can exceed kChunkSplitAbove keys.  Shorter spans run
-// unsplit: measured on MI355X, the merge launch costs more than the shorter
-// critical path saves (d24 1024-token prefill: 0.65 ms unsplit, 0.86 ms at
-// 512-key splits; a 16k-key GQA chunk batch: 7.95 ms at 512, 10.8 unsplit).
-constexpr int64_t kChunkKeysPerSplit = 512;
+// Chunk-kernel splits, used when a workgroup's span can exceed
+// kChunkSplitAbove keys (shorter spans run unsplit: measured on MI355X, the
+// merge launch costs more than the shorter critical path saves; d24 1024-token
+// prefill: 0.65 ms unsplit, 0.86 ms at 512-key splits).  The split size is a
+// multiple of kChunkSplitUnit chosen so that one row of the batch alone gives
+// about kChunkWGPerRow workgroups: many q tiles and heads per row need few
+// splits.  Measured (us per call): one 14k-key row, 16/4 heads x 128 tokens
+// (32 workgroups per split): 94 at 512, 78 at 2048; 4/4 heads (8 per split):
+// 34 at 512, 58 at 2048; C5's 16 chunk rows: 136 at 512, 121 at 2048.
+constexpr int64_t kChunkSplitUnit = 512;
+constexpr int64_t kChunkWGPerRow = 256;
 constexpr int64_t kChunkSplitAbove = 2048;
 // Decode with wide workgroups and no split: at most this many groups (one per
 // CU) and this many keys per row.
@@ -111,8 +116,15 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
     // one workgroup's keys span at most (window + its queries) or the cache length
     const int64_t qb = chunk_rows_per_wg() / hb;
     const int64_t span = a.window_left >= 0 ? std::min<int64_t>(a.t_max, int64_t(a.window_left) + qb) : a.t_max;
-    int64_t ckps = a.keys_per_split > 0 ? a.keys_per_split
-                                        : (span > kChunkSplitAbove ? kChunkKeysPerSplit : span);
+    int64_t ckps = a.keys_per_split;
+    if (ckps == 0) {
+      // workgroups of one row per split: q tiles x kv heads x head blocks
+      const int64_t per_row = (a.t_new + qb - 1) / qb * a.n_kv_heads * plan->n_hblocks;
+      const int64_t want = (span * per_row + kChunkWGPerRow - 1) / kChunkWGPerRow;
+      ckps = span > kChunkSplitAbove
+                 ? std::min(span, std::max(kChunkSplitUnit, (want + kChunkSplitUnit - 1) / kChunkSplitUnit * kChunkSplitUnit))
+                 : span;
+    }
     int64_t cns = (span + ckps - 1) / ckps;
     if (cns > cap) {
       ckps = ((span + cap - 1) / cap + 63) / 64 * 64;

@@ -96,6 +96,23 @@ def test_workspace_zero_for_single_split_and_window_caps_keys():
         _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((1 * 250 * 8 + 255) // 256) + 250 * 128 * 4
 
 
+def _chunk_workspace(pairs, splits, D=128):
+    return _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((pairs * splits * 8 + 255) // 256) + pairs * splits * D * 4
+
+
+def test_chunk_split_size_gives_each_row_about_256_workgroups():
+    lib = _ext.lib()
+    # 16/4 heads, 128 tokens: 8 q tiles x 4 kv heads = 32 workgroups per split of a row;
+    # 16384 keys * 32 / 256 = 2048-key splits -> 8 splits
+    a = _attn_args(B=1, T_new=128, T_max=16384, H=16, H_kv=4)
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(a)) == _chunk_workspace(128 * 16, 8)
+    # 4/4 heads: 2 q tiles x 4 kv heads = 8 per split -> 512-key splits (the unit) -> 32 splits
+    a = _attn_args(B=1, T_new=128, T_max=16384, H=4, H_kv=4)
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(a)) == _chunk_workspace(128 * 4, 32)
+    # spans up to 2048 keys run unsplit: no workspace
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(B=1, T_new=128, T_max=2048, H=4, H_kv=4))) == 0
+
+
 def test_invalid_arguments_are_rejected_before_launch():
     lib = _ext.lib()
     a = _attn_args()

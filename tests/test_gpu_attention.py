@@ -229,6 +229,13 @@ def test_mfma_chunk_matches_oracle(T_new, H, H_kv, D, seqlens, window, dtype):
     _check(200 + T_new, len(seqlens), T_new, H, H_kv, D, T_max, seqlens, window, q_dtype=dtype, cache_dtype=dtype)
 
 
+@pytest.mark.parametrize("H,H_kv", [(16, 4), (4, 4)])
+def test_mfma_chunk_default_split_of_long_spans(H, H_kv):
+    """Spans beyond 2048 keys with the library's split size (2048 keys for 16/4 heads, 512 for
+    4/4): one long row next to short ones, merged by the split-merge kernel."""
+    _check(260 + H, 3, 128, H, H_kv, 128, 6200, [6000, 100, 3000], -1)
+
+
 @pytest.mark.parametrize("window", [-1, 512])
 def test_mfma_chunk_c3_prefill(window):
     """C3 prefill shape: one row, 1024 tokens into an empty cache, 12 heads x 128 (S and L windows)."""
