@@ -64,9 +64,6 @@
 #ifndef NC_DECODE_NT_LOADS
 #define NC_DECODE_NT_LOADS 1    // 1: K/V loads carry the non-temporal hint (+12% measured)
 #endif
-#ifndef NC_DECODE_EVEN_SPLITS
-#define NC_DECODE_EVEN_SPLITS 0 // 1: every split of a row gets ceil(n / num_splits) keys (no empty splits)
-#endif
 #ifndef NC_DECODE_PV_DOT2
 #define NC_DECODE_PV_DOT2 1     // 1: P.V with v_dot2 on key pairs (packed caches)
 #endif
@@ -187,22 +184,20 @@ struct KeyRange {
   int qpos, lo, hi, n, nsplit, kps;
 };
 
+// A row's split size is keys_per_split, or, for rows longer than
+// num_splits * keys_per_split, the row spread evenly over the num_splits
+// splits (multiples of 64 keys): the grid is sized for num_splits per group
+// and no split of a long row is left without keys.
 __device__ __forceinline__ KeyRange key_range(const DecodeParams& p, int64_t b, int t) {
   KeyRange r;
   r.qpos = p.seqlens[b] + t;  // absolute position of the query
   r.hi = min(r.qpos + 1, p.t_max);
   r.lo = p.window >= 0 ? max(0, r.qpos - p.window) : 0;
   r.n = r.hi - r.lo;
-#if NC_DECODE_EVEN_SPLITS
-  r.kps = r.n > 0 ? ((r.n + p.num_splits - 1) / p.num_splits + 15) / 16 * 16 : p.keys_per_split;
-#else
   r.kps = p.keys_per_split;
-#endif
-#if NC_DECODE_EVEN_SPLITS
-  r.nsplit = r.n > 0 ? (r.n + r.kps - 1) / r.kps : 1;
-#else
+  if (r.n > r.kps * p.num_splits) r.kps = ((r.n + p.num_splits - 1) / p.num_splits + 63) / 64 * 64;
   r.nsplit = r.n > 0 ? static_cast<int>(fdiv(static_cast<uint32_t>(r.n + r.kps - 1), p.fd_kps)) : 1;
-#endif
+  if (r.kps != p.keys_per_split) r.nsplit = (r.n + r.kps - 1) / r.kps;
   return r;
 }
 

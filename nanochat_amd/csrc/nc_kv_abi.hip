@@ -26,6 +26,12 @@ constexpr int64_t kChunkMinTokens = 8;
 constexpr int64_t kChunkSplitUnit = 512;
 constexpr int64_t kChunkWGPerRow = 256;
 constexpr int64_t kChunkSplitAbove = 2048;
+// Default decode plans size their split count so the grid has about this
+// many workgroups (long rows then take longer splits).
+#ifndef NC_DECODE_GRID_TARGET
+#define NC_DECODE_GRID_TARGET 4096
+#endif
+constexpr int64_t kDecodeGridTarget = NC_DECODE_GRID_TARGET;
 // Decode with wide workgroups and no split: at most this many groups (one per
 // CU) and this many keys per row.
 constexpr int64_t kWideMinGroups = 128;
@@ -85,12 +91,16 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   if (kps == 0) {
     kps = std::max<int64_t>(64, (default_split_bytes() / (a.head_dim * ebytes) + 63) / 64 * 64);
   }
+  // Splits per group: enough for the longest possible row at kps keys, but at
+  // most max_splits() and, for the library default, at most about
+  // kDecodeGridTarget workgroups in all.  Rows longer than ns * kps are spread
+  // evenly over the ns splits by the kernels (multiples of 64 keys), so the
+  // grid follows the cache length only up to that bound: workgroups past a
+  // row's end still cost a dispatch each (48 rows x 128 keys, GQA 16/4: 9.5 us
+  // per call in a 4096-key cache, 20.2 us in a 16384-key one).
   const int64_t cap = max_splits();
-  int64_t ns = (max_keys + kps - 1) / kps;
-  if (ns > cap) {
-    kps = ((max_keys + cap - 1) / cap + 63) / 64 * 64;
-    ns = (max_keys + kps - 1) / kps;
-  }
+  const int64_t grid_cap = a.keys_per_split > 0 ? cap : std::max<int64_t>(1, kDecodeGridTarget / plan->n_groups);
+  int64_t ns = std::min((max_keys + kps - 1) / kps, std::min(cap, grid_cap));
   // Between half and one chip's worth of groups with short rows: one 8-wave
   // workgroup per group streams the whole row (no split, so no merge launch).
   // Measured on MI355X: d24 decode (192 groups x 513-1153 keys) 0.469 -> 0.391

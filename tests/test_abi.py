@@ -91,9 +91,23 @@ def test_workspace_zero_for_single_split_and_window_caps_keys():
     assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=256))) == 0
     assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=4096, window=255))) == 0
     assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(T_max=4096, window=256))) > 0
-    # split cap: 65536 keys at the 256-key default is exactly 256 splits; 80000 keys widen the split
+    # split cap: 65536 keys at the 256-key default is exactly 256 splits; 80000 keys keep 256
+    # splits (the kernels spread a longer row evenly over them)
     assert lib.nc_attn_workspace_bytes(ctypes.byref(_attn_args(B=1, H=1, H_kv=1, T_max=80000))) == \
-        _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((1 * 250 * 8 + 255) // 256) + 250 * 128 * 4
+        _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((1 * 256 * 8 + 255) // 256) + 256 * 128 * 4
+
+
+def test_default_decode_grid_is_bounded():
+    lib = _ext.lib()
+    # 192 (row, kv head) groups (48 rows, GQA 16/4 -> one head block of 4): 4096 // 192 = 21 splits
+    # per group instead of 16384 / 256 = 64; an explicit split size keeps every split
+    pairs = 48 * 16
+    a = _attn_args(B=48, T_max=16384, H=16, H_kv=4)
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(a)) == \
+        _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((pairs * 21 * 8 + 255) // 256) + pairs * 21 * 128 * 4
+    a = _attn_args(B=48, T_max=16384, H=16, H_kv=4, kps=256)
+    assert lib.nc_attn_workspace_bytes(ctypes.byref(a)) == \
+        _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((pairs * 64 * 8 + 255) // 256) + pairs * 64 * 128 * 4
 
 
 def _chunk_workspace(pairs, splits, D=128):

@@ -349,3 +349,12 @@ def test_decode_more_groups_than_counters_uses_merge_launch():
     seqlens = [(b * 37) % 200 for b in range(B)]
     _check(330, B, 1, H, H, 32, 200, seqlens, -1, kps=64)
     _sync_region_is_zero()
+
+
+def test_decode_long_rows_spread_over_bounded_splits():
+    """96 groups in a 16384-key cache: the default plan keeps 4096 // 96 = 42 splits per group, so
+    rows longer than 42 x 256 keys take longer splits (multiples of 64); short rows in the same
+    call keep 256-key splits."""
+    B = 24
+    seqlens = [16000, 12000, 7000, 2689, 128, 10751, 10752, 10753] + [(i * 331) % 900 for i in range(B - 8)]
+    _check(340, B, 1, 8, 4, 64, 16384, seqlens, -1)
