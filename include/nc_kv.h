@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NC_KV_ABI_VERSION 3
+#define NC_KV_ABI_VERSION 4
 
 /* Element types (the torch dtypes the reference path uses). */
 enum nc_dtype {
@@ -52,6 +52,17 @@ enum nc_status {
  * nanochat/flash_attention.py:161 for the same condition. */
 #define NC_DEVERR_OVERFLOW 1
 
+/* Bit set in *error_flag when cache_batch_idx[b] is outside [0, cache_batch).
+ * Nothing of batch row b is read, written or stored.  FA3's
+ * flash_attn_with_kvcache indexes the cache with it unchecked. */
+#define NC_DEVERR_BATCH_IDX 4
+
+/* cache_batch_idx (optional, FA3's flash_attn_with_kvcache argument): batch
+ * row b reads and appends cache row cache_batch_idx[b] instead of row b;
+ * cache_seqlens stays indexed by b.  cache_batch is the number of cache rows.
+ * With k/v given the indices must be distinct (rows sharing a cache row race,
+ * as in FA3). */
+
 /* ---------------------------------------------------------------------------
  * Ragged KV append: k_cache[b, cache_seqlens[b] + t] = k[b, t] (and v), t < t_new.
  * Replaces nanochat/flash_attention.py:160-162 with FA3's per-row positions
@@ -66,6 +77,8 @@ typedef struct nc_append_args {
   const void* v;
   const int32_t* cache_seqlens;  /* (B,) */
   int32_t* error_flag;           /* optional (NULL): NC_DEVERR_* bits are OR-ed in */
+  const int32_t* cache_batch_idx;  /* (B,) or NULL (row b is cache row b) */
+  int64_t cache_batch;           /* cache rows (with cache_batch_idx) */
   int64_t batch, t_new, t_max, n_kv_heads, head_dim;
   int64_t kc_stride_b, kc_stride_t, kc_stride_h;
   int64_t vc_stride_b, vc_stride_t, vc_stride_h;
@@ -131,6 +144,8 @@ typedef struct nc_attn_args {
   const void* v;
   const int32_t* cache_seqlens;  /* (B,) read-only */
   int32_t* error_flag;           /* optional */
+  const int32_t* cache_batch_idx;  /* (B,) or NULL (row b is cache row b) */
+  int64_t cache_batch;           /* cache rows (with cache_batch_idx) */
   void* workspace;
   size_t workspace_bytes;
   int64_t batch, t_new, t_max, n_heads, n_kv_heads, head_dim;

@@ -71,6 +71,8 @@ struct ChunkParams {
   const char* kc;
   const char* vc;
   const int32_t* seqlens;
+  const int32_t* cache_idx;  // cache_batch_idx or NULL
+  int64_t cache_batch;
   int64_t q_sb, q_st, q_sh;
   int64_t kc_sb, kc_st, kc_sh;
   int64_t vc_sb, vc_st, vc_sh;
@@ -167,6 +169,10 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int hb = static_cast<int>(rem);
   const int64_t b = fdivmod(gtmp, p.fd_kv_heads, rem);
   const int hk = static_cast<int>(rem);
+  // cache row of batch row b; an invalid index skips the row in every workgroup of it
+  const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err,
+                               qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0);
+  if (cb < 0) return;
 
   const int s = p.seqlens[b];
   const int q0 = qt * QB;
@@ -212,8 +218,8 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   for (int db = 0; db < DB; ++db) acc_o[db] = make_float4(0.f, 0.f, 0.f, 0.f);
 
   constexpr int EB = elem<TC>::kBytes;
-  const char* kbase = p.kc + (b * p.kc_sb + hk * p.kc_sh) * EB;
-  const char* vbase = p.vc + (b * p.vc_sb + hk * p.vc_sh) * EB;
+  const char* kbase = p.kc + (cb * p.kc_sb + hk * p.kc_sh) * EB;
+  const char* vbase = p.vc + (cb * p.vc_sb + hk * p.vc_sh) * EB;
   const int64_t kst = p.kc_st * EB;
   const int64_t vst = p.vc_st * EB;
   // new tokens: position j >= s is token j - s of k/v; this workgroup stores the
@@ -426,6 +432,7 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.q = a.q; p.out = a.out;
   p.kc = static_cast<const char*>(a.k_cache); p.vc = static_cast<const char*>(a.v_cache);
   p.seqlens = a.cache_seqlens;
+  p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;

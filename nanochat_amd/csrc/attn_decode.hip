@@ -94,6 +94,8 @@ struct DecodeParams {
   const void* v_new;
   const int32_t* seqlens;
   int32_t* err;
+  const int32_t* cache_idx;  // cache_batch_idx or NULL
+  int64_t cache_batch;
   float* part_ml;
   float* part_o;
   uint32_t* tickets;  // non-null: splits merge in-kernel (one zeroed counter per group)
@@ -253,6 +255,7 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
   typedef typename MergeVec<VE>::T VT;
   constexpr int TPH = D / VE;  // threads per head
   const GroupIdx gi = group_index(p, blockIdx.x);
+  if (cache_row(p.cache_idx, p.cache_batch, gi.b, nullptr, false) < 0) return;  // the row was skipped
   int nsplit;
   if (p.merge_qb == 0) {
     nsplit = key_range(p, gi.b, gi.t).nsplit;
@@ -387,6 +390,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   const GroupIdx gi = group_index(p, group);
   const int64_t b = gi.b;
   const int t = gi.t, hk = gi.hk, hb = gi.hb;
+  // cache row of batch row b; an invalid index skips the row in every workgroup of it
+  const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err,
+                               split == 0 && t == 0 && hk == 0 && hb == 0 && threadIdx.x == 0);
+  if (cb < 0) return;
 
   const KeyRange kr = key_range(p, b, t);
   const int64_t pair0 = (b * p.t_new + t) * p.n_heads + hk * p.group + hb * GB;  // (b, t, first q head)
@@ -423,8 +430,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     for (int e = 0; e < VEC; ++e) o[g][e] = 0.0f;
   }
 
-  const char* kbase = p.kc + (b * p.kc_sb + hk * p.kc_sh + col * VEC) * EB;
-  const char* vbase = p.vc + (b * p.vc_sb + hk * p.vc_sh + col * VEC) * EB;
+  const char* kbase = p.kc + (cb * p.kc_sb + hk * p.kc_sh + col * VEC) * EB;
+  const char* vbase = p.vc + (cb * p.vc_sb + hk * p.vc_sh + col * VEC) * EB;
   const int64_t kst = p.kc_st * EB;
   const int64_t vst = p.vc_st * EB;
 
@@ -807,6 +814,7 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.kc = static_cast<char*>(a.k_cache); p.vc = static_cast<char*>(a.v_cache);
   p.k_new = a.k; p.v_new = a.v;
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
+  p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.part_ml = s.part_ml; p.part_o = s.part_o;
   p.tickets = plan.merge_in_kernel ? s.tickets : nullptr;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;

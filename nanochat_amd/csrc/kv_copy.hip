@@ -19,6 +19,8 @@ struct AppendParams {
   const void* v;
   const int32_t* seqlens;
   int32_t* err;
+  const int32_t* cache_idx;  // cache_batch_idx or NULL
+  int64_t cache_batch;
   int64_t kc_sb, kc_st, kc_sh, vc_sb, vc_st, vc_sh;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
   int32_t t_new, t_max, h_kv, vecs_per_head;  // vecs_per_head = D / VEC
@@ -38,6 +40,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
   const int h = static_cast<int>(r % p.h_kv); r /= p.h_kv;
   const int t = static_cast<int>(r % p.t_new);
   const int64_t b = r / p.t_new;
+  const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, c == 0 && h == 0 && t == 0 && !is_v);
+  if (cb < 0) return;
   const int pos = p.seqlens[b] + t;
   if (pos < 0 || pos >= p.t_max) {
     if (p.err != nullptr && c == 0 && h == 0 && !is_v) atomicOr(p.err, NC_DEVERR_OVERFLOW);
@@ -48,8 +52,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
                             : (b * p.k_sb + t * p.k_st + h * p.k_sh);
   const uint4 val = load_as_cache_vec<T>(src, soff + static_cast<int64_t>(c) * VEC, p.in_dtype);
   char* dst = static_cast<char*>(is_v ? p.vc : p.kc);
-  const int64_t doff = is_v ? (b * p.vc_sb + pos * p.vc_st + h * p.vc_sh)
-                            : (b * p.kc_sb + pos * p.kc_st + h * p.kc_sh);
+  const int64_t doff = is_v ? (cb * p.vc_sb + pos * p.vc_st + h * p.vc_sh)
+                            : (cb * p.kc_sb + pos * p.kc_st + h * p.kc_sh);
   *reinterpret_cast<uint4*>(dst + (doff + static_cast<int64_t>(c) * VEC) * elem<T>::kBytes) = val;
 }
 
@@ -111,6 +115,8 @@ struct RopeAppendParams {
   char* vc;
   const int32_t* seqlens;
   int32_t* err;
+  const int32_t* cache_idx;  // cache_batch_idx or NULL
+  int64_t cache_batch;
   const void* cos;
   const void* sin;
   int64_t q_sb, q_st, q_sh, k_sb, k_st, k_sh, v_sb, v_st, v_sh;
@@ -171,16 +177,18 @@ __global__ __launch_bounds__(256) void qk_rope_append_kernel(const RopeAppendPar
     for (int e = 0; e < VE; ++e) store_any(p.q_out, o0 + e, p.q_dtype, x[e]);
     return;
   }
+  const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, c == 0 && h == 0 && t == 0 && kind == 1);
+  if (cb < 0) return;
   if (pos < 0 || pos >= p.t_max) {
     if (c == 0 && h == 0 && kind == 1 && p.err != nullptr) atomicOr(p.err, NC_DEVERR_OVERFLOW);
     return;
   }
   if (kind == 1) {
-    const int64_t d0 = b * p.kc_sb + static_cast<int64_t>(pos) * p.kc_st + h * p.kc_sh + c * VE;
+    const int64_t d0 = cb * p.kc_sb + static_cast<int64_t>(pos) * p.kc_st + h * p.kc_sh + c * VE;
 #pragma unroll
     for (int e = 0; e < VE; ++e) store_any(p.kc, d0 + e, p.cache_dtype, x[e]);
   } else {
-    const int64_t d0 = b * p.vc_sb + static_cast<int64_t>(pos) * p.vc_st + h * p.vc_sh + c * VE;
+    const int64_t d0 = cb * p.vc_sb + static_cast<int64_t>(pos) * p.vc_st + h * p.vc_sh + c * VE;
 #pragma unroll
     for (int e = 0; e < VE; ++e) copy_elem(p.vc, d0 + e, p.cache_dtype, p.v, soff + c * VE + e, p.q_dtype);
   }
@@ -192,6 +200,7 @@ hipError_t launch_append(const nc_append_args& a, hipStream_t stream) {
   AppendParams p;
   p.kc = a.k_cache; p.vc = a.v_cache; p.k = a.k; p.v = a.v;
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
+  p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
   p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
@@ -219,6 +228,7 @@ hipError_t launch_rope_append(const nc_attn_args& a, const nc_qk_prologue& pro, 
   p.q = a.q; p.q_out = q_out; p.k = a.k; p.v = a.v;
   p.kc = static_cast<char*>(a.k_cache); p.vc = static_cast<char*>(a.v_cache);
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
+  p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.cos = pro.cos; p.sin = pro.sin;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;

@@ -308,4 +308,18 @@ __device__ __forceinline__ ChunkSpan chunk_span(int s, int q0, int q_end, int t_
   return c;
 }
 
+// Cache row of batch row b: cache_batch_idx[b] when given (FA3's argument),
+// else b.  -1 when the index is outside [0, n_rows); `report` sets
+// NC_DEVERR_BATCH_IDX (one reporting thread per row keeps the atomics few).
+__device__ __forceinline__ int64_t cache_row(const int32_t* idx, int64_t n_rows, int64_t b, int32_t* err,
+                                             bool report) {
+  if (idx == nullptr) return b;
+  const int64_t r = idx[b];
+  if (r < 0 || r >= n_rows) {
+    if (report && err != nullptr) atomicOr(err, NC_DEVERR_BATCH_IDX);
+    return -1;
+  }
+  return r;
+}
+
 }  // namespace nckv

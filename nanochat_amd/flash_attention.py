@@ -67,7 +67,8 @@ def _dtype_code(t: torch.Tensor, name: str) -> int:
     return code
 
 
-def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_size, keys_per_split):
+def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_size, keys_per_split,
+               cache_batch_idx=None):
     """Validate the arguments of one attention call and fill nc_attn_args (workspace left empty)."""
     if cache_seqlens is None:
         raise ValueError(f"{name}: cache_seqlens is required")
@@ -79,8 +80,12 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
     Bc, T_max, H_kv, Dc = k_cache.shape
     if tuple(v_cache.shape) != (Bc, T_max, H_kv, Dc):
         raise ValueError(f"v_cache shape {tuple(v_cache.shape)} != k_cache shape {tuple(k_cache.shape)}")
-    if Bc != B or Dc != D:
+    if (cache_batch_idx is None and Bc != B) or Dc != D:
         raise ValueError(f"cache shape {tuple(k_cache.shape)} does not match q shape {tuple(q.shape)}")
+    if cache_batch_idx is not None:
+        if tuple(cache_batch_idx.shape) != (B,) or cache_batch_idx.dtype != torch.int32:
+            raise ValueError("cache_batch_idx must be a (B,) int32 tensor")
+        cache_batch_idx = cache_batch_idx.contiguous()
     if H % H_kv != 0:
         raise ValueError(f"n_heads {H} is not a multiple of n_kv_heads {H_kv}")
     if k is not None:
@@ -93,6 +98,7 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
     if k_cache.dtype != v_cache.dtype:
         raise TypeError("k_cache and v_cache must have the same dtype")
     tensors = [q, k_cache, v_cache, cache_seqlens] + ([k, v] if k is not None else [])
+    tensors += [cache_batch_idx] if cache_batch_idx is not None else []
     dev = _require_gpu(name, *tensors)
     for tname, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("k", k), ("v", v)):
         if t is not None and t.stride(-1) != 1:
@@ -109,6 +115,8 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
     a.v = v.data_ptr() if v is not None else None
     a.cache_seqlens = cache_seqlens.data_ptr()
     a.error_flag = _ext.error_flag(dev).data_ptr()
+    if cache_batch_idx is not None:
+        a.cache_batch_idx, a.cache_batch = cache_batch_idx.data_ptr(), Bc
     a.batch, a.t_new, a.t_max = B, T_new, T_max
     a.n_heads, a.n_kv_heads, a.head_dim = H, H_kv, D
     a.q_stride_b, a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
@@ -140,18 +148,22 @@ def _check_device_errors(name, dev):
             raise RuntimeError(f"{name}: cache_seqlens + T_new exceeds the cache length")
         if bits & _ext.NC_DEVERR_ROPE_RANGE:
             raise RuntimeError(f"{name}: a position is beyond the rotary tables")
+        if bits & _ext.NC_DEVERR_BATCH_IDX:
+            raise RuntimeError(f"{name}: cache_batch_idx holds an index outside the cache's batch dimension")
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
-                            causal=False, window_size=(-1, -1), *, keys_per_split: int = 0):
+                            causal=False, window_size=(-1, -1), *, cache_batch_idx=None, keys_per_split: int = 0):
     """Append k/v into the cache in place, then attend (see the module docstring).
 
-    q: (B, T_new, H, D); k_cache, v_cache: (B, T_max, H_kv, D);
+    q: (B, T_new, H, D); k_cache, v_cache: (B, T_max, H_kv, D), or (B_cache, T_max,
+    H_kv, D) with cache_batch_idx: (B,) int32, FA3's argument (row b uses cache
+    row cache_batch_idx[b]; indices must be distinct when k/v are given);
     k, v: (B, T_new, H_kv, D) or None; cache_seqlens: (B,) int32 on the GPU.
     Returns (B, T_new, H, D) in q's dtype.
     """
     a, out, dev, _ = _attn_call("flash_attn_with_kvcache", q, k_cache, v_cache, k, v, cache_seqlens, causal,
-                                window_size, keys_per_split)
+                                window_size, keys_per_split, cache_batch_idx)
     L = _ext.lib()
     ref = ctypes.byref(a)
     stream = _ext.stream_handle(dev)
@@ -163,7 +175,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
 
 def flash_attn_with_kvcache_rope(q, k_cache, v_cache, k, v, cache_seqlens, cos, sin, causal=True,
                                  window_size=(-1, -1), *, qk_scale: float = 1.2, eps=None,
-                                 keys_per_split: int = 0):
+                                 cache_batch_idx=None, keys_per_split: int = 0):
     """flash_attn_with_kvcache with nanochat's QK prologue fused (nanochat/gpt.py:98-102).
 
     q and k are the raw projections; inside the call each token t of row b is
@@ -190,7 +202,7 @@ def flash_attn_with_kvcache_rope(q, k_cache, v_cache, k, v, cache_seqlens, cos, 
     if not sin2.is_contiguous() or sin2.data_ptr() % 16 != 0:
         sin2 = sin2.clone(memory_format=torch.contiguous_format)
     a, out, dev, _ = _attn_call("flash_attn_with_kvcache_rope", q, k_cache, v_cache, k, v, cache_seqlens, causal,
-                                window_size, keys_per_split)
+                                window_size, keys_per_split, cache_batch_idx)
     _require_gpu("flash_attn_with_kvcache_rope", cos2, sin2)
     pro = _ext.QKPrologue()
     pro.cos, pro.sin = cos2.data_ptr(), sin2.data_ptr()

@@ -19,6 +19,14 @@ It restates, with the same torch operations the reference uses:
                                row's own position s_b (the fused prologue's contract;
                                the reference slices the table at row 0's position)
   - rotary_tables              nanochat/gpt.py:268-283
+  - cache_batch_idx            FA3's flash_attn_with_kvcache argument, reached through
+                               nanochat/flash_attention.py:149-153 (the FA3 branch;
+                               flash-attention 3 from the 'varunneal/flash-attention-3'
+                               kernel-hub build, not vendored): batch row b reads and
+                               appends cache row cache_batch_idx[b]; cache_seqlens
+                               stays indexed by b.  Pinned by the permutation
+                               identity in tests/test_oracle.py (no golden vectors:
+                               the reference never passes it).
 The pins for each function (brute force, closed forms, the reference's own
 known-answer test) live in tests/test_oracle.py.
 
@@ -77,24 +85,26 @@ def kv_append(k_cache, v_cache, k, v, cache_seqlens):
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
-                            causal=False, window_size=(-1, -1), compute_dtype=None):
+                            causal=False, window_size=(-1, -1), compute_dtype=None, cache_batch_idx=None):
     """nanochat/flash_attention.py:155-177, one batch row at a time.
 
     Mutates k_cache/v_cache like the reference.  ``compute_dtype`` (default:
     q's dtype) is the dtype q and the cache slices are cast to before SDPA;
-    the result is returned in q's dtype.
+    the result is returned in q's dtype.  ``cache_batch_idx`` (FA3): row b
+    uses cache row cache_batch_idx[b].
     """
     B, T_new, H, D = q.shape
     cdt = compute_dtype if compute_dtype is not None else q.dtype
     outs = []
     for b in range(B):
         pos = int(cache_seqlens[b])
+        c = int(cache_batch_idx[b]) if cache_batch_idx is not None else b
         if k is not None and v is not None:
-            k_cache[b:b + 1, pos:pos + T_new, :, :] = k[b:b + 1]
-            v_cache[b:b + 1, pos:pos + T_new, :, :] = v[b:b + 1]
+            k_cache[c:c + 1, pos:pos + T_new, :, :] = k[b:b + 1]
+            v_cache[c:c + 1, pos:pos + T_new, :, :] = v[b:b + 1]
         end_pos = pos + T_new
-        k_full = k_cache[b:b + 1, :end_pos, :, :].to(cdt)
-        v_full = v_cache[b:b + 1, :end_pos, :, :].to(cdt)
+        k_full = k_cache[c:c + 1, :end_pos, :, :].to(cdt)
+        v_full = v_cache[c:c + 1, :end_pos, :, :].to(cdt)
         q_sdpa = q[b:b + 1].to(cdt).transpose(1, 2)
         k_sdpa = k_full.transpose(1, 2)
         v_sdpa = v_full.transpose(1, 2)

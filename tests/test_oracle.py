@@ -193,6 +193,30 @@ def test_brute_force_detects_planted_gqa_mapping(monkeypatch):
 # ---------------------------------------------------------------------------
 # KVCache: nanochat's own tests (tests/test_engine.py:84-155) on the oracle cache
 # ---------------------------------------------------------------------------
+@pytest.mark.parametrize("T_new,with_kv", [(1, True), (5, True), (3, False)])
+def test_cache_batch_idx_is_a_row_permutation_of_the_cache(T_new, with_kv):
+    """FA3's cache_batch_idx: attending batch row b on cache row idx[b] equals attending on the
+    gathered cache C[idx] without indices; appends land in rows idx[b]; other rows are untouched."""
+    g = gen(401 + T_new)
+    Bc, B, T_max, H, H_kv, D = 5, 3, 24, 4, 2, 16
+    idx = torch.tensor([4, 0, 2], dtype=torch.int32)
+    kc = randn((Bc, T_max, H_kv, D), g, torch.float32)
+    vc = randn((Bc, T_max, H_kv, D), g, torch.float32)
+    q = randn((B, T_new, H, D), g, torch.float32)
+    k = randn((B, T_new, H_kv, D), g, torch.float32) if with_kv else None
+    v = randn((B, T_new, H_kv, D), g, torch.float32) if with_kv else None
+    sl = torch.tensor([7, 0, 19], dtype=torch.int32)
+    kc1, vc1 = kc.clone(), vc.clone()
+    out1 = orc.flash_attn_with_kvcache(q, kc1, vc1, k=k, v=v, cache_seqlens=sl, causal=True,
+                                       window_size=(6, 0), cache_batch_idx=idx)
+    kc2, vc2 = kc[idx.long()].clone(), vc[idx.long()].clone()
+    out2 = orc.flash_attn_with_kvcache(q, kc2, vc2, k=k, v=v, cache_seqlens=sl, causal=True, window_size=(6, 0))
+    assert torch.equal(out1, out2)
+    assert torch.equal(kc1[idx.long()], kc2) and torch.equal(vc1[idx.long()], vc2)
+    for r in (1, 3):
+        assert torch.equal(kc1[r], kc[r]) and torch.equal(vc1[r], vc[r])
+
+
 def test_oracle_kv_cache_basic():
     c = orc.KVCache(batch_size=2, num_heads=3, seq_len=64, head_dim=5, num_layers=6, device="cpu", dtype=torch.float32)
     assert c.get_pos() == 0
