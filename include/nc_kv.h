@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define NC_KV_ABI_VERSION 4
+#define NC_KV_ABI_VERSION 5
 
 /* Element types (the torch dtypes the reference path uses). */
 enum nc_dtype {
@@ -57,7 +57,18 @@ enum nc_status {
  * flash_attn_with_kvcache indexes the cache with it unchecked. */
 #define NC_DEVERR_BATCH_IDX 4
 
-/* cache_batch_idx (optional, FA3's flash_attn_with_kvcache argument): batch
+/* Bit set in *error_flag when row b's tokens [cu_seqlens_q[b],
+ * cu_seqlens_q[b+1]) are not a range inside [0, total_q) of at most t_new
+ * (max_seqlen_q) tokens.  Nothing of that row is read, written or stored. */
+#define NC_DEVERR_QLEN 8
+
+/* cu_seqlens_q (optional, FA3's varlen layout): q, k, v and out hold packed
+ * tokens (total_q, H or H_kv, D); batch row b owns tokens [cu_seqlens_q[b],
+ * cu_seqlens_q[b+1]) and appends them at cache_seqlens[b].  t_new is then the
+ * bound max_seqlen_q, the *_stride_b fields are ignored, and out is
+ * (total_q, H, D) contiguous.  A batch may mix rows of 0, 1 and many tokens.
+ *
+ * cache_batch_idx (optional, FA3's flash_attn_with_kvcache argument): batch
  * row b reads and appends cache row cache_batch_idx[b] instead of row b;
  * cache_seqlens stays indexed by b.  cache_batch is the number of cache rows.
  * With k/v given the indices must be distinct (rows sharing a cache row race,
@@ -79,6 +90,8 @@ typedef struct nc_append_args {
   int32_t* error_flag;           /* optional (NULL): NC_DEVERR_* bits are OR-ed in */
   const int32_t* cache_batch_idx;  /* (B,) or NULL (row b is cache row b) */
   int64_t cache_batch;           /* cache rows (with cache_batch_idx) */
+  const int32_t* cu_seqlens_q;   /* (B+1,) or NULL: packed new tokens */
+  int64_t total_q;               /* tokens in k, v (with cu_seqlens_q) */
   int64_t batch, t_new, t_max, n_kv_heads, head_dim;
   int64_t kc_stride_b, kc_stride_t, kc_stride_h;
   int64_t vc_stride_b, vc_stride_t, vc_stride_h;
@@ -146,6 +159,8 @@ typedef struct nc_attn_args {
   int32_t* error_flag;           /* optional */
   const int32_t* cache_batch_idx;  /* (B,) or NULL (row b is cache row b) */
   int64_t cache_batch;           /* cache rows (with cache_batch_idx) */
+  const int32_t* cu_seqlens_q;   /* (B+1,) or NULL: packed query tokens */
+  int64_t total_q;               /* tokens in q, k, v, out (with cu_seqlens_q) */
   void* workspace;
   size_t workspace_bytes;
   int64_t batch, t_new, t_max, n_heads, n_kv_heads, head_dim;

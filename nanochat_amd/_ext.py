@@ -16,13 +16,14 @@ import torch
 # NANOCHAT_AMD_LIB points at another build of the same library (e.g. a tuning
 # variant); by default the in-tree build next to this file is loaded.
 LIB_PATH = Path(os.environ.get("NANOCHAT_AMD_LIB", Path(__file__).resolve().parent / "libnc_kv.so"))
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 NC_DEVERR_OVERFLOW = 1
 NC_DEVERR_ROPE_RANGE = 2
 NC_DEVERR_BATCH_IDX = 4
+NC_DEVERR_QLEN = 8
 # leading workspace bytes holding split counters: zero before first use, left zero by every call
 NC_WORKSPACE_SYNC_BYTES = 65536
 
@@ -36,7 +37,7 @@ class AppendArgs(ctypes.Structure):
         ("k_cache", _c_void_p), ("v_cache", _c_void_p),
         ("k", _c_void_p), ("v", _c_void_p),
         ("cache_seqlens", _c_void_p), ("error_flag", _c_void_p),
-        ("cache_batch_idx", _c_void_p), ("cache_batch", _i64),
+        ("cache_batch_idx", _c_void_p), ("cache_batch", _i64), ("cu_seqlens_q", _c_void_p), ("total_q", _i64),
         ("batch", _i64), ("t_new", _i64), ("t_max", _i64), ("n_kv_heads", _i64), ("head_dim", _i64),
         ("kc_stride_b", _i64), ("kc_stride_t", _i64), ("kc_stride_h", _i64),
         ("vc_stride_b", _i64), ("vc_stride_t", _i64), ("vc_stride_h", _i64),
@@ -63,7 +64,7 @@ class AttnArgs(ctypes.Structure):
         ("k_cache", _c_void_p), ("v_cache", _c_void_p),
         ("k", _c_void_p), ("v", _c_void_p),
         ("cache_seqlens", _c_void_p), ("error_flag", _c_void_p),
-        ("cache_batch_idx", _c_void_p), ("cache_batch", _i64),
+        ("cache_batch_idx", _c_void_p), ("cache_batch", _i64), ("cu_seqlens_q", _c_void_p), ("total_q", _i64),
         ("workspace", _c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("batch", _i64), ("t_new", _i64), ("t_max", _i64),
         ("n_heads", _i64), ("n_kv_heads", _i64), ("head_dim", _i64),

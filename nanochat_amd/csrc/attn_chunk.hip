@@ -73,6 +73,8 @@ struct ChunkParams {
   const int32_t* seqlens;
   const int32_t* cache_idx;  // cache_batch_idx or NULL
   int64_t cache_batch;
+  const int32_t* cu_q;       // cu_seqlens_q (packed query tokens) or NULL
+  int64_t total_q;
   int64_t q_sb, q_st, q_sh;
   int64_t kc_sb, kc_st, kc_sh;
   int64_t vc_sb, vc_st, vc_sh;
@@ -174,11 +176,14 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
                                qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0);
   if (cb < 0) return;
 
-  const int s = p.seqlens[b];
+  const RowQ rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0);
   const int q0 = qt * QB;
-  const int q_end = min(q0 + QB, p.t_new);
+  if (q0 >= rq.len) return;  // no queries of this row in the tile (or the row was skipped)
+
+  const int s = p.seqlens[b];
+  const int q_end = min(q0 + QB, rq.len);
   if (p.fused && p.err != nullptr && qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0 &&
-      (s < 0 || s > p.t_max - p.t_new)) {
+      (s < 0 || s > p.t_max - rq.len)) {
     atomicOr(p.err, NC_DEVERR_OVERFLOW);  // a new token falls outside [0, t_max): not stored
   }
 
@@ -186,7 +191,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int row = wave * 16 + lr;
   const int qi = q0 + row / GB;
   const int h = hk * p.group + hb * GB + row % GB;
-  const bool row_ok = qi < p.t_new;
+  const bool row_ok = qi < rq.len;
   const int qpos = s + qi;
   const int row_lo = p.window >= 0 ? max(0, qpos - p.window) : 0;
 
@@ -196,13 +201,14 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   if (split >= span.nsplit) return;
   const int lo = span.lo + split * p.keys_per_split;
   const int hi = min(span.hi, lo + p.keys_per_split);
-  const int64_t pair_row = (b * p.t_new + qi) * p.n_heads + h;  // this lane's (query, head)
+  const int64_t pair_row = (b * p.t_new + qi) * p.n_heads + h;   // this lane's (query, head): partials
+  const int64_t out_row = (rq.tok0 + qi) * p.n_heads + h;        // its row of `out`
 
   // ---- Q^T fragments (B operand): lane holds Q[row][32c + 8*lq + e] ----
   v8 qf[DC];
   {
     const TC* qp = reinterpret_cast<const TC*>(static_cast<const char*>(p.q) +
-                                              (b * p.q_sb + static_cast<int64_t>(qi) * p.q_st + h * p.q_sh) *
+                                              (token_offset(p.cu_q, rq, b, qi, p.q_sb, p.q_st) + h * p.q_sh) *
                                                   elem<TC>::kBytes);
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
@@ -226,8 +232,8 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   // ones of its own queries, [s + q0, s + q_end), once per kv head (hb == 0)
   const int new_lo = p.fused ? s : INT32_MAX;
   const int own_lo = (p.fused && hb == 0) ? s + q0 : INT32_MAX;
-  const char* knew = p.k_new + (b * p.k_sb + hk * p.k_sh) * EB;
-  const char* vnew = p.v_new + (b * p.v_sb + hk * p.v_sh) * EB;
+  const char* knew = p.k_new + (token_offset(p.cu_q, rq, b, 0, p.k_sb, p.k_st) + hk * p.k_sh) * EB;
+  const char* vnew = p.v_new + (token_offset(p.cu_q, rq, b, 0, p.v_sb, p.v_st) + hk * p.v_sh) * EB;
   const int64_t knst = p.k_st * EB;
   const int64_t vnst = p.v_st * EB;
 
@@ -275,7 +281,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   // wave-uniform bounds of this wave's query rows: tiles wholly inside every
   // row's mask skip the per-element mask
   const int qi_first = q0 + (wave * 16) / GB, qi_last = q0 + (wave * 16 + 15) / GB;
-  const bool wave_rows_full = qi_last < p.t_new;
+  const bool wave_rows_full = qi_last < rq.len;
   const int qpos_first = s + qi_first, qpos_last = s + qi_last;
   auto tile_step = [&](int kt0, uint4 (&kr)[PER_THREAD], uint4 (&vr)[PER_THREAD]) {
     __syncthreads();  // previous tile's LDS reads are done
@@ -391,7 +397,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   }
   // ---- normalise and store: lane holds O[row][16db + 4lq + r] ----
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + pair_row * static_cast<int64_t>(D);
+  uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + out_row * static_cast<int64_t>(D);
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
     const float o4[4] = {acc_o[db].x * inv, acc_o[db].y * inv, acc_o[db].z * inv, acc_o[db].w * inv};
@@ -433,6 +439,7 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.kc = static_cast<const char*>(a.k_cache); p.vc = static_cast<const char*>(a.v_cache);
   p.seqlens = a.cache_seqlens;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
+  p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;

@@ -96,6 +96,8 @@ struct DecodeParams {
   int32_t* err;
   const int32_t* cache_idx;  // cache_batch_idx or NULL
   int64_t cache_batch;
+  const int32_t* cu_q;       // cu_seqlens_q (packed query tokens) or NULL
+  int64_t total_q;
   float* part_ml;
   float* part_o;
   uint32_t* tickets;  // non-null: splits merge in-kernel (one zeroed counter per group)
@@ -256,12 +258,14 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
   constexpr int TPH = D / VE;  // threads per head
   const GroupIdx gi = group_index(p, blockIdx.x);
   if (cache_row(p.cache_idx, p.cache_batch, gi.b, nullptr, false) < 0) return;  // the row was skipped
+  const RowQ rq = row_queries(p.cu_q, p.total_q, gi.b, p.t_new, nullptr, false);
+  if (gi.t >= rq.len) return;  // no such query in this row (or the row was skipped)
   int nsplit;
   if (p.merge_qb == 0) {
     nsplit = key_range(p, gi.b, gi.t).nsplit;
   } else {
     const int q0 = static_cast<int>(fdiv(static_cast<uint32_t>(gi.t), p.fd_qb)) * p.merge_qb;
-    nsplit = chunk_span(p.seqlens[gi.b], q0, min(q0 + p.merge_qb, p.t_new), p.t_max, p.window,
+    nsplit = chunk_span(p.seqlens[gi.b], q0, min(q0 + p.merge_qb, rq.len), p.t_max, p.window,
                         p.keys_per_split).nsplit;
   }
   // Decode splits with at most CH slots: load every allocated slot without
@@ -271,6 +275,7 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
   if (!eager && nsplit <= 1) return;
   const int lim = eager ? p.num_splits : nsplit;
   const int64_t pair0 = (gi.b * p.t_new + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;
+  const int64_t opair0 = (rq.tok0 + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;  // row of `out`
   for (int e = threadIdx.x; e < GB * TPH; e += blockDim.x) {
     const int g = e / TPH, d0 = (e % TPH) * VE;
     const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
@@ -320,7 +325,7 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
     }
     if (nsplit <= 1) return;  // the producer wrote this query's output
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    const int64_t o0 = (pair0 + g) * D + d0;
+    const int64_t o0 = (opair0 + g) * D + d0;
 #pragma unroll
     for (int v = 0; v < VE; ++v) store_any(p.out, o0 + v, p.q_dtype, O[v] * inv);
   }
@@ -394,9 +399,12 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err,
                                split == 0 && t == 0 && hk == 0 && hb == 0 && threadIdx.x == 0);
   if (cb < 0) return;
+  const RowQ rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, split == 0 && t == 0 && hk == 0 && hb == 0 && threadIdx.x == 0);
+  if (t >= rq.len) return;  // no such query in this row (or the row was skipped)
 
   const KeyRange kr = key_range(p, b, t);
-  const int64_t pair0 = (b * p.t_new + t) * p.n_heads + hk * p.group + hb * GB;  // (b, t, first q head)
+  const int64_t pair0 = (b * p.t_new + t) * p.n_heads + hk * p.group + hb * GB;  // (b, t, first q head): partials
+  const int64_t opair0 = (rq.tok0 + t) * p.n_heads + hk * p.group + hb * GB;     // its row of `out`
   if (split >= kr.nsplit) return;  // past this query's keys: the merge never reads this slot
   const int qpos = kr.qpos;
   const int k0 = kr.lo + split * kr.kps;
@@ -528,7 +536,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   // the first tile's K/V loads are in flight ----
 #pragma unroll
   for (int g = 0; g < GB; ++g) {
-    const int64_t qoff = b * p.q_sb + t * p.q_st + (h0 + g) * p.q_sh + col * VEC;
+    const int64_t qoff = token_offset(p.cu_q, rq, b, t, p.q_sb, p.q_st) + (h0 + g) * p.q_sh + col * VEC;
     if (p.rope) {
       float xf[VEC];
       if constexpr (QPK) {
@@ -560,8 +568,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
 
   // ---- the appended token (fused path): read from k/v, store into the cache ----
   if (own_new && wave == NW - 1) {
-    const int64_t koff = b * p.k_sb + hk * p.k_sh + col * VEC;
-    const int64_t voff = b * p.v_sb + hk * p.v_sh + col * VEC;
+    const int64_t koff = token_offset(p.cu_q, rq, b, 0, p.k_sb, p.k_st) + hk * p.k_sh + col * VEC;
+    const int64_t voff = token_offset(p.cu_q, rq, b, 0, p.v_sb, p.v_st) + hk * p.v_sh + col * VEC;
     uint4 kn;
     if (p.rope) {
       float xf[VEC];
@@ -654,7 +662,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
 #pragma unroll
       for (int w = 0; w < NW; ++w) acc += sm_o[w][g][d] * sm_w[w][g];
       const float L = sm_L[g];
-      store_any(p.out, (pair0 + g) * D + d, p.q_dtype, L > 0.0f ? acc / L : 0.0f);
+      store_any(p.out, (opair0 + g) * D + d, p.q_dtype, L > 0.0f ? acc / L : 0.0f);
     }
     return;
   }
@@ -732,7 +740,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
       M = mx;
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    store_any(p.out, (pair0 + g) * D + d, p.q_dtype, O * inv);
+    store_any(p.out, (opair0 + g) * D + d, p.q_dtype, O * inv);
   }
 }
 
@@ -815,6 +823,7 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.k_new = a.k; p.v_new = a.v;
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
+  p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
   p.part_ml = s.part_ml; p.part_o = s.part_o;
   p.tickets = plan.merge_in_kernel ? s.tickets : nullptr;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;

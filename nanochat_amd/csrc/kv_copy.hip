@@ -21,6 +21,8 @@ struct AppendParams {
   int32_t* err;
   const int32_t* cache_idx;  // cache_batch_idx or NULL
   int64_t cache_batch;
+  const int32_t* cu_q;       // cu_seqlens_q (packed new tokens) or NULL
+  int64_t total_q;
   int64_t kc_sb, kc_st, kc_sh, vc_sb, vc_st, vc_sh;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
   int32_t t_new, t_max, h_kv, vecs_per_head;  // vecs_per_head = D / VEC
@@ -42,14 +44,16 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
   const int64_t b = r / p.t_new;
   const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, c == 0 && h == 0 && t == 0 && !is_v);
   if (cb < 0) return;
+  const RowQ rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, c == 0 && h == 0 && t == 0 && !is_v);
+  if (t >= rq.len) return;
   const int pos = p.seqlens[b] + t;
   if (pos < 0 || pos >= p.t_max) {
     if (p.err != nullptr && c == 0 && h == 0 && !is_v) atomicOr(p.err, NC_DEVERR_OVERFLOW);
     return;
   }
   const void* src = is_v ? p.v : p.k;
-  const int64_t soff = is_v ? (b * p.v_sb + t * p.v_st + h * p.v_sh)
-                            : (b * p.k_sb + t * p.k_st + h * p.k_sh);
+  const int64_t soff = is_v ? token_offset(p.cu_q, rq, b, t, p.v_sb, p.v_st) + h * p.v_sh
+                            : token_offset(p.cu_q, rq, b, t, p.k_sb, p.k_st) + h * p.k_sh;
   const uint4 val = load_as_cache_vec<T>(src, soff + static_cast<int64_t>(c) * VEC, p.in_dtype);
   char* dst = static_cast<char*>(is_v ? p.vc : p.kc);
   const int64_t doff = is_v ? (cb * p.vc_sb + pos * p.vc_st + h * p.vc_sh)
@@ -117,6 +121,8 @@ struct RopeAppendParams {
   int32_t* err;
   const int32_t* cache_idx;  // cache_batch_idx or NULL
   int64_t cache_batch;
+  const int32_t* cu_q;       // cu_seqlens_q (packed tokens) or NULL
+  int64_t total_q;
   const void* cos;
   const void* sin;
   int64_t q_sb, q_st, q_sh, k_sb, k_st, k_sh, v_sb, v_st, v_sh;
@@ -160,19 +166,23 @@ __global__ __launch_bounds__(256) void qk_rope_append_kernel(const RopeAppendPar
   const int pos = p.seqlens[b] + t;
   const int kind = slot < p.n_heads ? 0 : (slot < p.n_heads + p.n_kv_heads ? 1 : 2);  // q, k, v
   const int h = kind == 0 ? slot : (kind == 1 ? slot - p.n_heads : slot - p.n_heads - p.n_kv_heads);
+  // every lane of a row group takes part in the prologue's shuffles, so rows
+  // past a row's query count still run it (on zeros) and skip their stores
+  const RowQ rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, live && c == 0 && t == 0 && slot == 0);
+  const bool active = live && t < rq.len;
   const void* src = kind == 0 ? p.q : (kind == 1 ? p.k : p.v);
-  const int64_t soff = kind == 0 ? b * p.q_sb + t * p.q_st + h * p.q_sh
-                                 : (kind == 1 ? b * p.k_sb + t * p.k_st + h * p.k_sh
-                                              : b * p.v_sb + t * p.v_st + h * p.v_sh);
+  const int64_t soff = kind == 0 ? token_offset(p.cu_q, rq, b, t, p.q_sb, p.q_st) + h * p.q_sh
+                                 : (kind == 1 ? token_offset(p.cu_q, rq, b, t, p.k_sb, p.k_st) + h * p.k_sh
+                                              : token_offset(p.cu_q, rq, b, t, p.v_sb, p.v_st) + h * p.v_sh);
   float x[VE];
 #pragma unroll
-  for (int e = 0; e < VE; ++e) x[e] = live ? load_any(src, soff + c * VE + e, p.q_dtype) : 0.0f;
+  for (int e = 0; e < VE; ++e) x[e] = active ? load_any(src, soff + c * VE + e, p.q_dtype) : 0.0f;
   const int row = min(max(pos, 0), p.rot_len - 1);
   qk_prologue_lanes<G, VE>(x, c, p.cos, p.sin, row, p.rot_dtype, p.scale, p.eps);  // every lane takes part
-  if (!live) return;
+  if (!active) return;
   if (kind == 0) {
     if (c == 0 && (pos < 0 || pos >= p.rot_len) && p.err != nullptr) atomicOr(p.err, NC_DEVERR_ROPE_RANGE);
-    const int64_t o0 = ((b * p.t_new + t) * p.n_heads + h) * D + c * VE;
+    const int64_t o0 = ((rq.tok0 + t) * p.n_heads + h) * D + c * VE;
 #pragma unroll
     for (int e = 0; e < VE; ++e) store_any(p.q_out, o0 + e, p.q_dtype, x[e]);
     return;
@@ -201,6 +211,7 @@ hipError_t launch_append(const nc_append_args& a, hipStream_t stream) {
   p.kc = a.k_cache; p.vc = a.v_cache; p.k = a.k; p.v = a.v;
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
+  p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
   p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
@@ -229,6 +240,7 @@ hipError_t launch_rope_append(const nc_attn_args& a, const nc_qk_prologue& pro, 
   p.kc = static_cast<char*>(a.k_cache); p.vc = static_cast<char*>(a.v_cache);
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
+  p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
   p.cos = pro.cos; p.sin = pro.sin;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;

@@ -73,6 +73,7 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   if (!decode_supports(a.cache_dtype, a.head_dim)) return NC_ERR_HEAD_DIM;
   if (a.keys_per_split < 0 || a.keys_per_split % 64 != 0) return NC_ERR_BAD_SHAPE;
   if (a.cache_batch_idx != nullptr && a.cache_batch <= 0) return NC_ERR_BAD_SHAPE;
+  if (a.cu_seqlens_q != nullptr && (a.total_q < 0 || a.total_q > INT32_MAX)) return NC_ERR_BAD_SHAPE;
 
   const int group = static_cast<int>(a.n_heads / a.n_kv_heads);
   int hb = 1;
@@ -196,6 +197,7 @@ int nc_kv_append(const nc_append_args* args, void* stream) {
     return NC_ERR_BAD_SHAPE;
   }
   if (a.cache_batch_idx != nullptr && a.cache_batch <= 0) return NC_ERR_BAD_SHAPE;
+  if (a.cu_seqlens_q != nullptr && (a.total_q < 0 || a.total_q > INT32_MAX)) return NC_ERR_BAD_SHAPE;
   if (!valid_dtype(a.in_dtype) || !valid_dtype(a.cache_dtype)) return NC_ERR_DTYPE;
   const int64_t eb = dtype_bytes(a.cache_dtype);
   if ((a.head_dim * eb) % 16 != 0) return NC_ERR_HEAD_DIM;
@@ -289,6 +291,7 @@ int run_attention(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch
       ap.k_cache = a.k_cache; ap.v_cache = a.v_cache; ap.k = a.k; ap.v = a.v;
       ap.cache_seqlens = a.cache_seqlens; ap.error_flag = a.error_flag;
       ap.cache_batch_idx = a.cache_batch_idx; ap.cache_batch = a.cache_batch;
+      ap.cu_seqlens_q = a.cu_seqlens_q; ap.total_q = a.total_q;
       ap.batch = a.batch; ap.t_new = a.t_new; ap.t_max = a.t_max;
       ap.n_kv_heads = a.n_kv_heads; ap.head_dim = a.head_dim;
       ap.kc_stride_b = a.kc_stride_b; ap.kc_stride_t = a.kc_stride_t; ap.kc_stride_h = a.kc_stride_h;

@@ -322,4 +322,31 @@ __device__ __forceinline__ int64_t cache_row(const int32_t* idx, int64_t n_rows,
   return r;
 }
 
+// Queries of batch row b.  With cu_seqlens_q (packed tokens, FA3's varlen
+// layout) they are tokens [cu[b], cu[b+1]); without, row b holds t_new
+// queries starting at token b * t_new.  A range that is not inside
+// [0, total_q) or longer than t_new (the launch's bound, max_seqlen_q) gives
+// len = -1: the row is skipped and `report` sets NC_DEVERR_QLEN.
+struct RowQ {
+  int64_t tok0;  // token index of the row's first query (row of `out`)
+  int len;       // queries of the row
+};
+__device__ __forceinline__ RowQ row_queries(const int32_t* cu, int64_t total_q, int64_t b, int t_new, int32_t* err,
+                                            bool report) {
+  if (cu == nullptr) return RowQ{b * t_new, t_new};
+  const int a = cu[b], e = cu[b + 1];
+  if (a < 0 || e < a || e - a > t_new || e > total_q) {
+    if (report && err != nullptr) atomicOr(err, NC_DEVERR_QLEN);
+    return RowQ{a, -1};
+  }
+  return RowQ{a, e - a};
+}
+
+// Element offset of query/new token t of row b in q, k or v (batch stride sb
+// and token stride st; packed tokens ignore sb).
+__device__ __forceinline__ int64_t token_offset(const int32_t* cu, const RowQ& rq, int64_t b, int t, int64_t sb,
+                                                int64_t st) {
+  return cu != nullptr ? (rq.tok0 + t) * st : b * sb + t * st;
+}
+
 }  // namespace nckv

@@ -68,15 +68,35 @@ def _dtype_code(t: torch.Tensor, name: str) -> int:
 
 
 def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_size, keys_per_split,
-               cache_batch_idx=None):
-    """Validate the arguments of one attention call and fill nc_attn_args (workspace left empty)."""
+               cache_batch_idx=None, cu_seqlens_q=None, max_seqlen_q=None):
+    """Validate the arguments of one attention call and fill nc_attn_args (workspace left empty).
+
+    With cu_seqlens_q, q/k/v are packed tokens (total_q, H or H_kv, D) and the
+    output is (total_q, H, D); otherwise (B, T_new, ...).
+    """
     if cache_seqlens is None:
         raise ValueError(f"{name}: cache_seqlens is required")
     if (k is None) != (v is None):
         raise ValueError(f"{name}: pass both k and v, or neither")
-    if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
-        raise ValueError(f"{name}: q, k_cache, v_cache must be 4-D (B, T, H, D)")
-    B, T_new, H, D = q.shape
+    if k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise ValueError(f"{name}: k_cache, v_cache must be 4-D (B, T_max, H_kv, D)")
+    varlen = cu_seqlens_q is not None
+    if varlen:
+        if q.dim() != 3:
+            raise ValueError(f"{name}: with cu_seqlens_q, q must be (total_q, H, D)")
+        if max_seqlen_q is None:
+            raise ValueError(f"{name}: max_seqlen_q is required with cu_seqlens_q")
+        if cu_seqlens_q.dim() != 1 or cu_seqlens_q.dtype != torch.int32 or cu_seqlens_q.numel() < 2:
+            raise ValueError(f"{name}: cu_seqlens_q must be a (B+1,) int32 tensor")
+        cu_seqlens_q = cu_seqlens_q.contiguous()
+        total_q, H, D = q.shape
+        B, T_new = cu_seqlens_q.numel() - 1, int(max_seqlen_q)
+        if T_new < 1:
+            raise ValueError(f"{name}: max_seqlen_q must be >= 1")
+    else:
+        if q.dim() != 4:
+            raise ValueError(f"{name}: q must be 4-D (B, T, H, D)")
+        B, T_new, H, D = q.shape
     Bc, T_max, H_kv, Dc = k_cache.shape
     if tuple(v_cache.shape) != (Bc, T_max, H_kv, Dc):
         raise ValueError(f"v_cache shape {tuple(v_cache.shape)} != k_cache shape {tuple(k_cache.shape)}")
@@ -89,8 +109,9 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
     if H % H_kv != 0:
         raise ValueError(f"n_heads {H} is not a multiple of n_kv_heads {H_kv}")
     if k is not None:
-        if tuple(k.shape) != (B, T_new, H_kv, D) or tuple(v.shape) != (B, T_new, H_kv, D):
-            raise ValueError(f"k/v must have shape {(B, T_new, H_kv, D)}, got {tuple(k.shape)}, {tuple(v.shape)}")
+        kv_shape = (total_q, H_kv, D) if varlen else (B, T_new, H_kv, D)
+        if tuple(k.shape) != kv_shape or tuple(v.shape) != kv_shape:
+            raise ValueError(f"k/v must have shape {kv_shape}, got {tuple(k.shape)}, {tuple(v.shape)}")
         if k.dtype != q.dtype or v.dtype != q.dtype:
             raise TypeError(f"k/v dtype ({k.dtype}, {v.dtype}) must equal q dtype {q.dtype}")
     if tuple(cache_seqlens.shape) != (B,) or cache_seqlens.dtype != torch.int32:
@@ -99,6 +120,7 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
         raise TypeError("k_cache and v_cache must have the same dtype")
     tensors = [q, k_cache, v_cache, cache_seqlens] + ([k, v] if k is not None else [])
     tensors += [cache_batch_idx] if cache_batch_idx is not None else []
+    tensors += [cu_seqlens_q] if varlen else []
     dev = _require_gpu(name, *tensors)
     for tname, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("k", k), ("v", v)):
         if t is not None and t.stride(-1) != 1:
@@ -106,7 +128,7 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
     if not cache_seqlens.is_contiguous():
         cache_seqlens = cache_seqlens.contiguous()
 
-    out = torch.empty((B, T_new, H, D), dtype=q.dtype, device=dev)
+    out = torch.empty((total_q, H, D) if varlen else (B, T_new, H, D), dtype=q.dtype, device=dev)
     window = int(window_size[0]) if window_size is not None else -1
     a = _ext.AttnArgs()
     a.q = q.data_ptr(); a.out = out.data_ptr()
@@ -117,12 +139,20 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
     a.error_flag = _ext.error_flag(dev).data_ptr()
     if cache_batch_idx is not None:
         a.cache_batch_idx, a.cache_batch = cache_batch_idx.data_ptr(), Bc
+    if varlen:
+        a.cu_seqlens_q, a.total_q = cu_seqlens_q.data_ptr(), total_q
     a.batch, a.t_new, a.t_max = B, T_new, T_max
     a.n_heads, a.n_kv_heads, a.head_dim = H, H_kv, D
-    a.q_stride_b, a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    if varlen:  # packed tokens: token stride and head stride (the batch stride is unused)
+        a.q_stride_b, a.q_stride_t, a.q_stride_h = 0, q.stride(0), q.stride(1)
+    else:
+        a.q_stride_b, a.q_stride_t, a.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
     a.kc_stride_b, a.kc_stride_t, a.kc_stride_h = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
     a.vc_stride_b, a.vc_stride_t, a.vc_stride_h = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
-    if k is not None:
+    if k is not None and varlen:
+        a.k_stride_b, a.k_stride_t, a.k_stride_h = 0, k.stride(0), k.stride(1)
+        a.v_stride_b, a.v_stride_t, a.v_stride_h = 0, v.stride(0), v.stride(1)
+    elif k is not None:
         a.k_stride_b, a.k_stride_t, a.k_stride_h = k.stride(0), k.stride(1), k.stride(2)
         a.v_stride_b, a.v_stride_t, a.v_stride_h = v.stride(0), v.stride(1), v.stride(2)
     a.window_left = window if window >= 0 else -1
@@ -150,20 +180,26 @@ def _check_device_errors(name, dev):
             raise RuntimeError(f"{name}: a position is beyond the rotary tables")
         if bits & _ext.NC_DEVERR_BATCH_IDX:
             raise RuntimeError(f"{name}: cache_batch_idx holds an index outside the cache's batch dimension")
+        if bits & _ext.NC_DEVERR_QLEN:
+            raise RuntimeError(f"{name}: cu_seqlens_q holds a row outside [0, total_q) or longer than max_seqlen_q")
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
-                            causal=False, window_size=(-1, -1), *, cache_batch_idx=None, keys_per_split: int = 0):
+                            causal=False, window_size=(-1, -1), *, cache_batch_idx=None, cu_seqlens_q=None,
+                            max_seqlen_q=None, keys_per_split: int = 0):
     """Append k/v into the cache in place, then attend (see the module docstring).
 
     q: (B, T_new, H, D); k_cache, v_cache: (B, T_max, H_kv, D), or (B_cache, T_max,
     H_kv, D) with cache_batch_idx: (B,) int32, FA3's argument (row b uses cache
     row cache_batch_idx[b]; indices must be distinct when k/v are given);
     k, v: (B, T_new, H_kv, D) or None; cache_seqlens: (B,) int32 on the GPU.
-    Returns (B, T_new, H, D) in q's dtype.
+    cu_seqlens_q: (B+1,) int32 with max_seqlen_q (FA3's varlen layout): q, k, v
+    are packed tokens (total_q, H or H_kv, D), row b owning tokens
+    [cu[b], cu[b+1]); rows may hold 0, 1 or many tokens.
+    Returns (B, T_new, H, D), or (total_q, H, D) with cu_seqlens_q, in q's dtype.
     """
     a, out, dev, _ = _attn_call("flash_attn_with_kvcache", q, k_cache, v_cache, k, v, cache_seqlens, causal,
-                                window_size, keys_per_split, cache_batch_idx)
+                                window_size, keys_per_split, cache_batch_idx, cu_seqlens_q, max_seqlen_q)
     L = _ext.lib()
     ref = ctypes.byref(a)
     stream = _ext.stream_handle(dev)
@@ -175,7 +211,8 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
 
 def flash_attn_with_kvcache_rope(q, k_cache, v_cache, k, v, cache_seqlens, cos, sin, causal=True,
                                  window_size=(-1, -1), *, qk_scale: float = 1.2, eps=None,
-                                 cache_batch_idx=None, keys_per_split: int = 0):
+                                 cache_batch_idx=None, cu_seqlens_q=None, max_seqlen_q=None,
+                                 keys_per_split: int = 0):
     """flash_attn_with_kvcache with nanochat's QK prologue fused (nanochat/gpt.py:98-102).
 
     q and k are the raw projections; inside the call each token t of row b is
@@ -202,7 +239,7 @@ def flash_attn_with_kvcache_rope(q, k_cache, v_cache, k, v, cache_seqlens, cos, 
     if not sin2.is_contiguous() or sin2.data_ptr() % 16 != 0:
         sin2 = sin2.clone(memory_format=torch.contiguous_format)
     a, out, dev, _ = _attn_call("flash_attn_with_kvcache_rope", q, k_cache, v_cache, k, v, cache_seqlens, causal,
-                                window_size, keys_per_split, cache_batch_idx)
+                                window_size, keys_per_split, cache_batch_idx, cu_seqlens_q, max_seqlen_q)
     _require_gpu("flash_attn_with_kvcache_rope", cos2, sin2)
     pro = _ext.QKPrologue()
     pro.cos, pro.sin = cos2.data_ptr(), sin2.data_ptr()

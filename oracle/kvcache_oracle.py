@@ -27,6 +27,11 @@ It restates, with the same torch operations the reference uses:
                                stays indexed by b.  Pinned by the permutation
                                identity in tests/test_oracle.py (no golden vectors:
                                the reference never passes it).
+  - cu_seqlens_q               FA3's varlen layout through the same branch: packed
+                               tokens, row b owning [cu[b], cu[b+1]); restated as one
+                               call per row of the function above, pinned by the
+                               uniform-length and per-row identities in
+                               tests/test_oracle.py.
 The pins for each function (brute force, closed forms, the reference's own
 known-answer test) live in tests/test_oracle.py.
 
@@ -85,14 +90,32 @@ def kv_append(k_cache, v_cache, k, v, cache_seqlens):
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
-                            causal=False, window_size=(-1, -1), compute_dtype=None, cache_batch_idx=None):
+                            causal=False, window_size=(-1, -1), compute_dtype=None, cache_batch_idx=None,
+                            cu_seqlens_q=None):
     """nanochat/flash_attention.py:155-177, one batch row at a time.
 
     Mutates k_cache/v_cache like the reference.  ``compute_dtype`` (default:
     q's dtype) is the dtype q and the cache slices are cast to before SDPA;
     the result is returned in q's dtype.  ``cache_batch_idx`` (FA3): row b
-    uses cache row cache_batch_idx[b].
+    uses cache row cache_batch_idx[b].  ``cu_seqlens_q`` (FA3 varlen): q, k, v
+    are packed tokens (total_q, H, D) and row b owns [cu[b], cu[b+1]); the
+    output is packed the same way.
     """
+    if cu_seqlens_q is not None:
+        outs = []
+        for b in range(len(cu_seqlens_q) - 1):
+            a, e = int(cu_seqlens_q[b]), int(cu_seqlens_q[b + 1])
+            if e == a:
+                continue
+            c = int(cache_batch_idx[b]) if cache_batch_idx is not None else b
+            y = flash_attn_with_kvcache(q[a:e].unsqueeze(0), k_cache, v_cache,
+                                        k=k[a:e].unsqueeze(0) if k is not None else None,
+                                        v=v[a:e].unsqueeze(0) if v is not None else None,
+                                        cache_seqlens=cache_seqlens[b:b + 1], causal=causal,
+                                        window_size=window_size, compute_dtype=compute_dtype,
+                                        cache_batch_idx=torch.tensor([c], dtype=torch.int32))
+            outs.append(y[0])
+        return torch.cat(outs, dim=0) if outs else q.new_empty((0,) + tuple(q.shape[1:]))
     B, T_new, H, D = q.shape
     cdt = compute_dtype if compute_dtype is not None else q.dtype
     outs = []

@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_header_constants_match_python_mirror():
     text = HEADER.read_text()
     for name in ("NC_KV_ABI_VERSION", "NC_WORKSPACE_SYNC_BYTES", "NC_DEVERR_OVERFLOW", "NC_DEVERR_ROPE_RANGE",
-                 "NC_DEVERR_BATCH_IDX"):
+                 "NC_DEVERR_BATCH_IDX", "NC_DEVERR_QLEN"):
         value = int(re.search(r"#define %s (\d+)" % name, text).group(1))
         py = _ext.ABI_VERSION if name == "NC_KV_ABI_VERSION" else getattr(_ext, name)
         assert py == value, name

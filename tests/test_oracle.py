@@ -217,6 +217,45 @@ def test_cache_batch_idx_is_a_row_permutation_of_the_cache(T_new, with_kv):
         assert torch.equal(kc1[r], kc[r]) and torch.equal(vc1[r], vc[r])
 
 
+def test_varlen_uniform_lengths_equal_the_fixed_length_call():
+    """cu_seqlens_q with every row holding T tokens is the (B, T, ...) call on flattened tokens."""
+    g = gen(410)
+    B, T, T_max, H, H_kv, D = 3, 4, 30, 4, 2, 16
+    q, k, v = (randn((B, T, h, D), g, torch.float32) for h in (H, H_kv, H_kv))
+    kc, vc = randn((B, T_max, H_kv, D), g, torch.float32), randn((B, T_max, H_kv, D), g, torch.float32)
+    sl = torch.tensor([3, 0, 20], dtype=torch.int32)
+    cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32)
+    kc1, vc1, kc2, vc2 = kc.clone(), vc.clone(), kc.clone(), vc.clone()
+    o1 = orc.flash_attn_with_kvcache(q.reshape(B * T, H, D), kc1, vc1, k=k.reshape(B * T, H_kv, D),
+                                     v=v.reshape(B * T, H_kv, D), cache_seqlens=sl, causal=True,
+                                     window_size=(5, 0), cu_seqlens_q=cu)
+    o2 = orc.flash_attn_with_kvcache(q, kc2, vc2, k=k, v=v, cache_seqlens=sl, causal=True, window_size=(5, 0))
+    assert torch.equal(o1, o2.reshape(B * T, H, D))
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+
+
+def test_varlen_mixed_lengths_equal_one_call_per_row():
+    """Rows of 0, 1 and several tokens: each row's output and appends equal a B=1 call of its own."""
+    g = gen(411)
+    lens, T_max, H, H_kv, D = [2, 0, 1, 5], 40, 4, 4, 8
+    cu = torch.tensor([0, 2, 2, 3, 8], dtype=torch.int32)
+    total = int(cu[-1])
+    q, k, v = (randn((total, h, D), g, torch.float32) for h in (H, H_kv, H_kv))
+    kc, vc = randn((4, T_max, H_kv, D), g, torch.float32), randn((4, T_max, H_kv, D), g, torch.float32)
+    sl = torch.tensor([7, 30, 0, 11], dtype=torch.int32)
+    kc1, vc1 = kc.clone(), vc.clone()
+    out = orc.flash_attn_with_kvcache(q, kc1, vc1, k=k, v=v, cache_seqlens=sl, causal=True, cu_seqlens_q=cu)
+    assert out.shape == (total, H, D)
+    for b, n in enumerate(lens):
+        a = int(cu[b])
+        kb, vb = kc[b:b + 1].clone(), vc[b:b + 1].clone()
+        if n:
+            ob = orc.flash_attn_with_kvcache(q[a:a + n][None], kb, vb, k=k[a:a + n][None], v=v[a:a + n][None],
+                                             cache_seqlens=sl[b:b + 1], causal=True)
+            assert torch.equal(out[a:a + n], ob[0])
+        assert torch.equal(kc1[b], kb[0]) and torch.equal(vc1[b], vb[0])
+
+
 def test_oracle_kv_cache_basic():
     c = orc.KVCache(batch_size=2, num_heads=3, seq_len=64, head_dim=5, num_layers=6, device="cpu", dtype=torch.float32)
     assert c.get_pos() == 0
