@@ -23,7 +23,8 @@ LIB_PATH = PKG_DIR / LIB_NAME
 OBJ_DIR = PKG_DIR / "_build"
 ARCH = "gfx950"
 
-SOURCES = ["nc_kv_abi.hip", "kv_copy.hip", "attn_decode.hip", "attn_chunk.hip"]
+SOURCES = ["nc_kv_abi.hip", "kv_copy.hip", "attn_decode.hip", "attn_decode_bf16.hip", "attn_decode_f16.hip",
+           "attn_decode_f32.hip", "attn_chunk.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -62,7 +63,7 @@ def build(verbose: bool = True, defines: dict | None = None, out: Path | None = 
     extra = tuple(f"-D{k}={v}" for k, v in sorted((defines or {}).items()))
     obj_dir = OBJ_DIR if not extra else OBJ_DIR / ("v_" + "_".join(f"{k}{v}" for k, v in sorted(defines.items())))
     obj_dir.mkdir(parents=True, exist_ok=True)
-    workers = min(len(SOURCES), max(1, (os.cpu_count() or 2) // 2), 8)
+    workers = min(len(SOURCES), os.cpu_count() or 2, 8)
     with ThreadPoolExecutor(max_workers=workers) as ex:
         objs = list(ex.map(lambda s: _compile(s, obj_dir, extra), SOURCES))
     tmp = out.with_suffix(".so.tmp")

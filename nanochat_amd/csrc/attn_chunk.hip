@@ -75,6 +75,7 @@ struct ChunkParams {
   int64_t cache_batch;
   const int32_t* cu_q;       // cu_seqlens_q (packed query tokens) or NULL
   int64_t total_q;
+  int32_t indirect;          // cache_idx or cu_q given: per-row lookups (else row b, t_new queries)
   int64_t q_sb, q_st, q_sh;
   int64_t kc_sb, kc_st, kc_sh;
   int64_t vc_sb, vc_st, vc_sh;
@@ -132,7 +133,9 @@ template <> struct mfma_t<f16> {
   }
 };
 
-template <typename TC, int D, int GB>
+// IND: the launch passes cache_batch_idx or cu_seqlens_q (per-row lookups);
+// plain launches use kernels without the lookup code (3% on the C5 batch).
+template <typename TC, int D, int GB, bool IND>
 __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const ChunkParams p) {
   typedef typename mfma_t<TC>::v8 v8;
   constexpr int QB = kRows / GB;          // queries per workgroup
@@ -171,12 +174,16 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int hb = static_cast<int>(rem);
   const int64_t b = fdivmod(gtmp, p.fd_kv_heads, rem);
   const int hk = static_cast<int>(rem);
-  // cache row of batch row b; an invalid index skips the row in every workgroup of it
-  const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err,
-                               qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0);
-  if (cb < 0) return;
-
-  const RowQ rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0);
+  // cache row and queries of batch row b (cache_batch_idx, cu_seqlens_q); an
+  // invalid entry skips the row in every workgroup of it
+  int64_t cb = b;
+  RowQ rq{b * p.t_new, p.t_new};
+  if constexpr (IND) {
+    const bool report = qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0;
+    cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
+    if (cb < 0) return;
+    rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, report);
+  }
   const int q0 = qt * QB;
   if (q0 >= rq.len) return;  // no queries of this row in the tile (or the row was skipped)
 
@@ -408,17 +415,22 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   }
 }
 
-template <typename TC, int D>
-hipError_t launch_c(const ChunkParams& p, int gb, hipStream_t stream) {
+template <typename TC, int D, bool IND>
+hipError_t launch_ci(const ChunkParams& p, int gb, hipStream_t stream) {
   const int64_t n_wg = static_cast<int64_t>(kXcdsC) * p.n_qtiles * p.num_splits * ((p.n_groups + kXcdsC - 1) / kXcdsC);
   const dim3 grid(static_cast<unsigned>(n_wg)), block(kChunkWaves * kWave);
   switch (gb) {
-    case 8: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 8>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 4>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 2>), grid, block, 0, stream, p); break;
-    default: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 1>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 8, IND>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 4, IND>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 2, IND>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 1, IND>), grid, block, 0, stream, p); break;
   }
   return hipGetLastError();
+}
+
+template <typename TC, int D>
+hipError_t launch_c(const ChunkParams& p, int gb, hipStream_t stream) {
+  return p.indirect ? launch_ci<TC, D, true>(p, gb, stream) : launch_ci<TC, D, false>(p, gb, stream);
 }
 
 }  // namespace
@@ -440,6 +452,7 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.seqlens = a.cache_seqlens;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
+  p.indirect = (a.cache_batch_idx != nullptr || a.cu_seqlens_q != nullptr) ? 1 : 0;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
