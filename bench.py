@@ -204,7 +204,8 @@ def run_c4(dev, stream, steps, kps=0, ckps=0):
 
 def run_c5(dev, stream, steps, kps=0, ckps=0):
     """GQA mixed batch: 32 layers, 16 q / 4 kv x 128, B=64, Zipf(1.2) lengths; rows 0-47 decode,
-    rows 48-63 chunk-append 128 tokens each step (two calls per layer on row-slice views)."""
+    rows 48-63 chunk-append 128 tokens each step: two calls per layer on row-slice views, and the
+    same step as one varlen call per layer (cu_seqlens_q over the packed tokens)."""
     import numpy as np
     from nanochat_amd.flash_attention import flash_attn_with_kvcache
     L, H, HKV, D, B, T, C, ND = 32, 16, 4, 128, 64, 16384, 128, 48
@@ -216,12 +217,16 @@ def run_c5(dev, stream, steps, kps=0, ckps=0):
         g.manual_seed(0)
         kc = torch.empty((L, B, T, HKV, D), device=dev, dtype=torch.bfloat16).normal_(generator=g)
         vc = torch.empty_like(kc).normal_(generator=g)
-        qd = torch.randn((steps, L, ND, 1, H, D), generator=g, device=dev, dtype=torch.bfloat16)
-        kd, vd = (torch.randn((steps, L, ND, 1, HKV, D), generator=g, device=dev, dtype=torch.bfloat16)
+        # packed tokens per (step, layer): 48 decode tokens, then 16 rows x 128 chunk tokens; the
+        # two-call legs use views of the same data
+        NT = ND + (B - ND) * C
+        qp = torch.randn((steps, L, NT, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        kp, vp = (torch.randn((steps, L, NT, HKV, D), generator=g, device=dev, dtype=torch.bfloat16)
                   for _ in range(2))
-        qc = torch.randn((steps, L, B - ND, C, H, D), generator=g, device=dev, dtype=torch.bfloat16)
-        kch, vch = (torch.randn((steps, L, B - ND, C, HKV, D), generator=g, device=dev, dtype=torch.bfloat16)
-                    for _ in range(2))
+        qd, kd, vd = (x[:, :, :ND].unflatten(2, (ND, 1)) for x in (qp, kp, vp))
+        qc, kch, vch = (x[:, :, ND:].unflatten(2, (B - ND, C)) for x in (qp, kp, vp))
+        lens = torch.tensor([1] * ND + [C] * (B - ND), dtype=torch.int32, device=dev)
+        cu = torch.cat([torch.zeros(1, dtype=torch.int32, device=dev), lens.cumsum(0).to(torch.int32)])
         sl = s0.to(dev)
         s0d = s0.to(dev)
 
@@ -240,9 +245,18 @@ def run_c5(dev, stream, steps, kps=0, ckps=0):
                                         keys_per_split=ckps)
             sl[ND:].add_(C)
 
+    def varlen_body():
+        for i in range(steps):
+            for layer in range(L):
+                flash_attn_with_kvcache(qp[i, layer], kc[layer], vc[layer], k=kp[i, layer], v=vp[i, layer],
+                                        cache_seqlens=sl, causal=True, window_size=(-1, 0), cu_seqlens_q=cu,
+                                        max_seqlen_q=C)
+            sl.add_(lens)
+
     reset = lambda: sl.copy_(s0d)  # noqa: E731
     ms_dec = _graph_time(stream, dec_body, reset)
     ms_chunk = _graph_time(stream, chunk_body, reset)
+    ms_varlen = _graph_time(stream, varlen_body, reset)
     dec_bytes = sum(_kv_bytes((s0[:ND] + i).tolist(), [-1] * L, HKV, H, D) for i in range(steps))
     flops = 0
     for i in range(steps):
@@ -256,7 +270,8 @@ def run_c5(dev, stream, steps, kps=0, ckps=0):
             "decode_pct_of_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
             "chunk_ms_per_step": round(ms_chunk / steps, 4), "chunk_TFLOP_per_s": round(tflops, 1),
             "chunk_pct_of_bf16_peak": round(100 * tflops / 2500.0, 2),
-            "step_ms": round((ms_dec + ms_chunk) / steps, 4), "seqlens_mean": float(s0.float().mean())}
+            "step_ms": round((ms_dec + ms_chunk) / steps, 4),
+            "varlen_one_call_step_ms": round(ms_varlen / steps, 4), "seqlens_mean": float(s0.float().mean())}
 
 
 def run_c3(dev, stream, steps, kps=0, ckps=0):

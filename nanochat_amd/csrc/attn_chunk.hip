@@ -76,6 +76,7 @@ struct ChunkParams {
   const int32_t* cu_q;       // cu_seqlens_q (packed query tokens) or NULL
   int64_t total_q;
   int32_t indirect;          // cache_idx or cu_q given: per-row lookups (else row b, t_new queries)
+  int32_t q_bound, len_lo, len_hi;  // varlen rows: validity bound, and the token counts this launch takes
   int64_t q_sb, q_st, q_sh;
   int64_t kc_sb, kc_st, kc_sh;
   int64_t vc_sb, vc_st, vc_sh;
@@ -182,7 +183,8 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     const bool report = qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0;
     cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
     if (cb < 0) return;
-    rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, report);
+    rq = row_queries(p.cu_q, p.total_q, b, p.q_bound, p.err, report);
+    if (rq.len < p.len_lo || rq.len > p.len_hi) return;  // another launch's row (or skipped)
   }
   const int q0 = qt * QB;
   if (q0 >= rq.len) return;  // no queries of this row in the tile (or the row was skipped)
@@ -445,7 +447,8 @@ bool chunk_supports(const nc_attn_args& a) {
 
 int chunk_rows_per_wg() { return kRows; }
 
-hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream) {
+hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream,
+                        const RowFilter* rows) {
   ChunkParams p;
   p.q = a.q; p.out = a.out;
   p.kc = static_cast<const char*>(a.k_cache); p.vc = static_cast<const char*>(a.v_cache);
@@ -453,6 +456,13 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
   p.indirect = (a.cache_batch_idx != nullptr || a.cu_seqlens_q != nullptr) ? 1 : 0;
+  p.q_bound = p.len_hi = static_cast<int32_t>(a.t_new);
+  p.len_lo = 0;
+  if (rows != nullptr) {
+    p.len_lo = rows->lo;
+    p.len_hi = rows->hi;
+    p.q_bound = rows->bound;
+  }
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;

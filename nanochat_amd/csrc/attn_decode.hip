@@ -47,6 +47,8 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
   p.indirect = (a.cache_batch_idx != nullptr || a.cu_seqlens_q != nullptr) ? 1 : 0;
+  p.q_bound = p.len_hi = static_cast<int32_t>(a.t_new);
+  p.len_lo = 0;
   p.part_ml = s.part_ml; p.part_o = s.part_o;
   p.tickets = plan.merge_in_kernel ? s.tickets : nullptr;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
@@ -94,8 +96,13 @@ hipError_t launch_merge_d(const DecodeParams& p, int gb, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
-                              hipStream_t stream) {
+                              hipStream_t stream, const RowFilter* rows) {
   DecodeParams p = make_params(a, plan, s, false);
+  if (rows != nullptr) {
+    p.len_lo = rows->lo;
+    p.len_hi = rows->hi;
+    p.q_bound = rows->bound;
+  }
   p.tickets = nullptr;
   p.num_splits = plan.chunk_splits;
   p.keys_per_split = plan.chunk_keys_per_split;
@@ -110,8 +117,14 @@ hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const
 }
 
 hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
-                         bool fused_append, const nc_qk_prologue* prologue, hipStream_t stream) {
+                         bool fused_append, const nc_qk_prologue* prologue, hipStream_t stream,
+                         const RowFilter* rows) {
   DecodeParams p = make_params(a, plan, s, fused_append);
+  if (rows != nullptr) {
+    p.len_lo = rows->lo;
+    p.len_hi = rows->hi;
+    p.q_bound = rows->bound;
+  }
   if (prologue != nullptr) {
     p.rope = 1;
     p.rope_cos = prologue->cos;

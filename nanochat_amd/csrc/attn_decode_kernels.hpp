@@ -91,6 +91,7 @@ struct DecodeParams {
   const int32_t* cu_q;       // cu_seqlens_q (packed query tokens) or NULL
   int64_t total_q;
   int32_t indirect;          // cache_idx or cu_q given: per-row lookups (else row b, t_new queries)
+  int32_t q_bound, len_lo, len_hi;  // varlen rows: validity bound, and the token counts this launch takes
   float* part_ml;
   float* part_o;
   uint32_t* tickets;  // non-null: splits merge in-kernel (one zeroed counter per group)
@@ -269,8 +270,9 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
   RowQ rq{gi.b * p.t_new, p.t_new};
   if constexpr (IND) {
     if (cache_row(p.cache_idx, p.cache_batch, gi.b, nullptr, false) < 0) return;  // the row was skipped
-    rq = row_queries(p.cu_q, p.total_q, gi.b, p.t_new, nullptr, false);
-    if (gi.t >= rq.len) return;  // no such query in this row (or the row was skipped)
+    rq = row_queries(p.cu_q, p.total_q, gi.b, p.q_bound, nullptr, false);
+    // no such query in this row, the row is another launch's, or it was skipped
+    if (rq.len < p.len_lo || rq.len > p.len_hi || gi.t >= rq.len) return;
   }
   int nsplit;
   if (p.merge_qb == 0) {
@@ -424,8 +426,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     const bool report = split == 0 && t == 0 && hk == 0 && hb == 0 && threadIdx.x == 0;
     cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
     if (cb < 0) return;
-    rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, report);
-    if (t >= rq.len) return;  // no such query in this row (or the row was skipped)
+    rq = row_queries(p.cu_q, p.total_q, b, p.q_bound, p.err, report);
+    // no such query in this row, the row is another launch's, or it was skipped
+    if (rq.len < p.len_lo || rq.len > p.len_hi || t >= rq.len) return;
   }
 
   const KeyRange kr = key_range(p, b, t);

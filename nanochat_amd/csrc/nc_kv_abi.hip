@@ -159,9 +159,25 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   } else {
     plan->ml_bytes = plan->o_bytes = 0;
   }
+  // A varlen batch on the chunk kernel sends its single-token rows to the
+  // decode kernel (a t_new = 1 plan of their own, partials after the chunk
+  // partials): on the chunk kernel each of them fills 1 query of a 16-query
+  // tile (C5 as one call per layer: 12.4 ms/step on the chunk kernel alone,
+  // two calls 7.2).
+  plan->split_rows = a.cu_seqlens_q != nullptr && plan->use_chunk;
+  plan->dec_bytes = 0;
+  if (plan->split_rows) {
+    nc_attn_args d = a;
+    d.t_new = 1;
+    AttnPlan dp;
+    const int st = plan_attention(d, &dp);
+    if (st != NC_OK) return st;
+    plan->dec_bytes = dp.ml_bytes + dp.o_bytes;
+  }
   // every non-empty workspace starts with the sync region, whether or not
   // this call uses it, so no call's scratch ever lands on the counters
-  plan->total_bytes = plan->ml_bytes + plan->o_bytes > 0 ? NC_WORKSPACE_SYNC_BYTES + plan->ml_bytes + plan->o_bytes : 0;
+  const size_t scratch = plan->ml_bytes + plan->o_bytes + plan->dec_bytes;
+  plan->total_bytes = scratch > 0 ? NC_WORKSPACE_SYNC_BYTES + scratch : 0;
   return NC_OK;
 }
 
@@ -303,8 +319,23 @@ int run_attention(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch
     }
   }
   if (plan.use_chunk) {
-    if (launch_chunk(a, plan, s, hs) != hipSuccess) return NC_ERR_LAUNCH;
-    if (plan.chunk_splits > 1 && launch_chunk_merge(a, plan, s, hs) != hipSuccess) return NC_ERR_LAUNCH;
+    RowFilter chunk_rows{0, static_cast<int>(a.t_new), static_cast<int>(a.t_new)};
+    if (plan.split_rows) {
+      // single-token rows on the decode kernel, the others on the chunk kernel
+      nc_attn_args d = a;
+      d.t_new = 1;
+      AttnPlan dp;
+      if (plan_attention(d, &dp) != NC_OK) return NC_ERR_BAD_SHAPE;
+      AttnScratch ds = s;
+      char* base = static_cast<char*>(a.workspace) + NC_WORKSPACE_SYNC_BYTES + plan.ml_bytes + plan.o_bytes;
+      ds.part_ml = reinterpret_cast<float*>(base);
+      ds.part_o = reinterpret_cast<float*>(base + dp.ml_bytes);
+      const RowFilter dec_rows{1, 1, static_cast<int>(a.t_new)};
+      if (launch_decode(d, dp, ds, fused, nullptr, hs, &dec_rows) != hipSuccess) return NC_ERR_LAUNCH;
+      chunk_rows.lo = 2;
+    }
+    if (launch_chunk(a, plan, s, hs, &chunk_rows) != hipSuccess) return NC_ERR_LAUNCH;
+    if (plan.chunk_splits > 1 && launch_chunk_merge(a, plan, s, hs, &chunk_rows) != hipSuccess) return NC_ERR_LAUNCH;
     return NC_OK;
   }
   return launch_decode(a, plan, s, fused, prologue, hs) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
@@ -318,7 +349,9 @@ size_t rope_q_bytes(const nc_attn_args& a) {
 }
 
 // Workspace offset of the prologue's q (after the sync region and partials).
-size_t rope_q_offset(const AttnPlan& plan) { return NC_WORKSPACE_SYNC_BYTES + plan.ml_bytes + plan.o_bytes; }
+size_t rope_q_offset(const AttnPlan& plan) {
+  return NC_WORKSPACE_SYNC_BYTES + plan.ml_bytes + plan.o_bytes + plan.dec_bytes;
+}
 
 // Workspace bytes of nc_attn_kvcache_rope.
 size_t rope_need(const nc_attn_args& a, const AttnPlan& plan) {

@@ -31,7 +31,11 @@ struct AttnPlan {
   bool use_chunk;      // T_new > 1 on the MFMA chunk kernel
   int chunk_keys_per_split;
   int chunk_splits;    // > 1: chunk partials merged by the split-merge kernel
-  size_t ml_bytes, o_bytes, total_bytes;
+  // varlen batch on the chunk kernel: its single-token rows run on the decode
+  // kernel (a t_new = 1 plan of their own; dec_bytes of partials after the
+  // chunk partials)
+  bool split_rows;
+  size_t ml_bytes, o_bytes, dec_bytes, total_bytes;
 };
 
 // Returns NC_OK and fills `plan`, or an error code.
@@ -40,8 +44,16 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan);
 hipError_t launch_append(const nc_append_args& a, hipStream_t stream);
 hipError_t launch_fanout(const nc_fanout_args& a, int unit_bytes, hipStream_t stream);
 // prologue != nullptr: the fused QK prologue on q and the appended k (t_new == 1 with k/v).
+// Rows one launch takes from a varlen batch (cu_seqlens_q) that is split
+// between the kernels: rows whose token count len satisfies lo <= len <= hi;
+// `bound` (the call's max_seqlen_q) is the validity limit of len.
+struct RowFilter {
+  int lo, hi, bound;
+};
+
 hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
-                         bool fused_append, const nc_qk_prologue* prologue, hipStream_t stream);
+                         bool fused_append, const nc_qk_prologue* prologue, hipStream_t stream,
+                         const RowFilter* rows = nullptr);
 // QK prologue for t_new > 1: q -> q_out (contiguous (B, T, H, D), q's dtype), k (transformed) and
 // v appended into the cache.
 hipError_t launch_rope_append(const nc_attn_args& a, const nc_qk_prologue& pro, void* q_out, hipStream_t stream);
@@ -49,11 +61,12 @@ hipError_t launch_rope_append(const nc_attn_args& a, const nc_qk_prologue& pro, 
 bool decode_supports(int cache_dtype, int64_t head_dim);
 bool decode_wide_supported(int head_block, int64_t head_dim);
 bool chunk_supports(const nc_attn_args& a);
-hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream);
+hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream,
+                        const RowFilter* rows = nullptr);
 int chunk_rows_per_wg();
 // Split merge of the chunk kernel's partials (plan.chunk_splits > 1).
 hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
-                              hipStream_t stream);
+                              hipStream_t stream, const RowFilter* rows = nullptr);
 int max_splits();
 int default_split_bytes();
 int64_t decode_grid(int64_t n_groups, int num_splits);

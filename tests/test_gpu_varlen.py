@@ -137,3 +137,12 @@ def test_varlen_malformed_rows_are_skipped_and_flagged():
                                       compute_dtype=torch.float32, cu_seqlens_q=torch.tensor([0, 1], dtype=torch.int32))
     assert max_rel_err(out[:1], ref.float()) <= 2e-2
     assert torch.equal(bits(kc_d), bits(ref_kc)) and torch.equal(bits(vc_d), bits(ref_vc))
+
+
+@pytest.mark.parametrize("kps", [0, 64])
+def test_varlen_mixed_batch_splits_single_token_rows_to_the_decode_kernel(kps):
+    """Single-token rows next to chunk rows: the decode kernel takes the former and the chunk kernel
+    the latter, each with split-K partials in its own workspace region (64-key splits)."""
+    lens = [1, 1, 40, 1, 0, 9, 1, 1, 128]
+    seqlens = [3000, 17, 2500, 1, 700, 2999, 64, 1500, 800]
+    _check(660 + kps, lens, seqlens, 16, 4, 128, 3200, kps=kps)
