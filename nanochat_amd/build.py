@@ -36,6 +36,15 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
+# Per-source flags.  The MFMA chunk kernel keeps its accumulators in VGPRs
+# (the MFMA forms that read and write VGPRs): with the compiler's default
+# AGPR accumulators every key tile copied the 32 output values to VGPRs and
+# back for the softmax rescale, and the kernel held 2 waves per SIMD instead
+# of 3.
+SOURCE_FLAGS = {
+    "attn_chunk.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+}
+
 
 def _hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -46,7 +55,8 @@ def _hipcc() -> str:
 
 def _compile(src: str, obj_dir: Path, extra: tuple) -> Path:
     obj = obj_dir / (Path(src).stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src, ()), *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+           str(CSRC / src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")

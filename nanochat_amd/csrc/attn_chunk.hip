@@ -99,14 +99,15 @@ struct ChunkParams {
   int32_t fused;
 };
 
+// MFMA accumulators as the builtin's own vector type (no float4 round trips,
+// which cost AGPR <-> VGPR copies around every MFMA).
+typedef float f4v __attribute__((ext_vector_type(4)));
+
 template <typename TC> struct mfma_t;
 template <> struct mfma_t<bf16> {
   typedef __bf16 v8 __attribute__((ext_vector_type(8)));
-  __device__ __forceinline__ static void run(const v8& a, const v8& b, float4& c) {
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    f4 acc = {c.x, c.y, c.z, c.w};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
-    c = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  __device__ __forceinline__ static void run(const v8& a, const v8& b, f4v& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint16_t from_float(float x) { return f32_to_bf16_rne(x); }
   // two values rounded to nearest even, packed (v_cvt_pk_bf16_f32)
@@ -119,11 +120,8 @@ template <> struct mfma_t<bf16> {
 };
 template <> struct mfma_t<f16> {
   typedef _Float16 v8 __attribute__((ext_vector_type(8)));
-  __device__ __forceinline__ static void run(const v8& a, const v8& b, float4& c) {
-    typedef float f4 __attribute__((ext_vector_type(4)));
-    f4 acc = {c.x, c.y, c.z, c.w};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
-    c = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  __device__ __forceinline__ static void run(const v8& a, const v8& b, f4v& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
   __device__ __forceinline__ static uint16_t from_float(float x) { return f32_to_f16_rne(x); }
   __device__ __forceinline__ static uint32_t pack2(float a, float b) {
@@ -228,9 +226,9 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   }
 
   float m_run = kNegBigC, l_run = 0.0f;
-  float4 acc_o[DB];
+  f4v acc_o[DB];
 #pragma unroll
-  for (int db = 0; db < DB; ++db) acc_o[db] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int db = 0; db < DB; ++db) acc_o[db] = f4v{0.f, 0.f, 0.f, 0.f};
 
   constexpr int EB = elem<TC>::kBytes;
   const char* kbase = p.kc + (cb * p.kc_sb + hk * p.kc_sh) * EB;
@@ -314,10 +312,10 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     if (kt0 + kBN < hi) load_regs(kt0 + kBN, kr, vr);
 
     // ---- S^T = K . Q^T for the 4 key blocks of the tile ----
-    float4 acc_s[4];
+    f4v acc_s[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      acc_s[kb] = make_float4(0.f, 0.f, 0.f, 0.f);
+      acc_s[kb] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
         const uint4 a = *reinterpret_cast<const uint4*>(ks + (16 * kb + lr) * KROW + (32 * c + 8 * lq) * 2);
@@ -332,7 +330,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     float mt = -__builtin_inff();
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const float a4[4] = {acc_s[kb].x, acc_s[kb].y, acc_s[kb].z, acc_s[kb].w};
+      const float a4[4] = {acc_s[kb][0], acc_s[kb][1], acc_s[kb][2], acc_s[kb][3]};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         sv[kb][r] = a4[r] * p.scale_log2;
@@ -368,7 +366,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     if (__any(m_new != m_run)) {
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        acc_o[db].x *= alpha; acc_o[db].y *= alpha; acc_o[db].z *= alpha; acc_o[db].w *= alpha;
+        acc_o[db] *= alpha;
       }
     }
     m_run = m_new;
@@ -384,8 +382,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
         const char* src1 = src0 + 16 * VROW;
         const i16x4 lo4 = lds_read_tr16(src0);
         const i16x4 hi4 = lds_read_tr16(src1);
-        const uint2 a = __builtin_bit_cast(uint2, lo4), c = __builtin_bit_cast(uint2, hi4);
-        const v8 av = __builtin_bit_cast(v8, make_uint4(a.x, a.y, c.x, c.y));
+        const v8 av = __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
         mfma_t<TC>::run(av, bp, acc_o[db]);
       }
     }
@@ -398,7 +395,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     // ---- partials for the merge kernel: o unnormalised, (m, l) once per row ----
     float* po = p.part_o + (pair_row * p.num_splits + split) * D;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) *reinterpret_cast<float4*>(po + 16 * db + 4 * lq) = acc_o[db];
+    for (int db = 0; db < DB; ++db) *reinterpret_cast<f4v*>(po + 16 * db + 4 * lq) = acc_o[db];
     if (lq == 0) {
       *reinterpret_cast<float2*>(p.part_ml + (pair_row * p.num_splits + split) * 2) = make_float2(m_run, l_run);
     }
@@ -409,7 +406,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + out_row * static_cast<int64_t>(D);
 #pragma unroll
   for (int db = 0; db < DB; ++db) {
-    const float o4[4] = {acc_o[db].x * inv, acc_o[db].y * inv, acc_o[db].z * inv, acc_o[db].w * inv};
+    const float o4[4] = {acc_o[db][0] * inv, acc_o[db][1] * inv, acc_o[db][2] * inv, acc_o[db][3] * inv};
     uint2 w;
     w.x = static_cast<uint32_t>(mfma_t<TC>::from_float(o4[0])) | (static_cast<uint32_t>(mfma_t<TC>::from_float(o4[1])) << 16);
     w.y = static_cast<uint32_t>(mfma_t<TC>::from_float(o4[2])) | (static_cast<uint32_t>(mfma_t<TC>::from_float(o4[3])) << 16);
