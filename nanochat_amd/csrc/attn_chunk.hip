@@ -151,7 +151,9 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int wave = tid / kWave;
+  // the wave index, provably wave-uniform (so tile bounds and masks derived
+  // from it compile to scalar branches, not per-lane exec masking)
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lq = lane / 16;               // lane group 0..3
   const int lr = lane % 16;
 

@@ -398,7 +398,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int wave = tid / kWave;
+  // the wave index, provably wave-uniform (so tile bounds and masks derived
+  // from it compile to scalar branches, not per-lane exec masking)
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int row = lane / LPK;
   const int col = lane % LPK;
 
