@@ -78,6 +78,15 @@ constexpr int kFanoutUnitsPerThread = 4;
 // grid: x over the per-layer region, y = layer, z = K/V.  Each thread loads
 // kFanoutUnitsPerThread units of the source once and stores them into every
 // destination row.
+// Non-temporal store of one copy unit (the fan-out writes far more than the
+// L2s hold and nothing reads it back in the same launch).
+__device__ __forceinline__ void store_nt(uint4* p, const uint4& v) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
+}
+__device__ __forceinline__ void store_nt(uint32_t* p, uint32_t v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void store_nt(uint16_t* p, uint16_t v) { __builtin_nontemporal_store(v, p); }
+
 template <typename U>
 __global__ __launch_bounds__(256) void kv_fanout_kernel(const FanoutParams p) {
   if (p.seqlens != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
@@ -88,18 +97,22 @@ __global__ __launch_bounds__(256) void kv_fanout_kernel(const FanoutParams p) {
   const U* src = reinterpret_cast<const U*>(p.src[z] + l * p.src_stride_l);
   char* dst_layer = p.dst[z] + l * p.dst_stride_l;
   const int64_t base = static_cast<int64_t>(blockIdx.x) * blockDim.x * kFanoutUnitsPerThread + threadIdx.x;
+  // every element defined on every path, so the values stay in registers
+  // (a conditionally written array was placed in LDS by the compiler and
+  // re-read, bank-conflicted, for each destination row)
   U val[kFanoutUnitsPerThread];
+  bool in[kFanoutUnitsPerThread];
 #pragma unroll
   for (int u = 0; u < kFanoutUnitsPerThread; ++u) {
     const int64_t idx = base + static_cast<int64_t>(u) * blockDim.x;
-    if (idx < p.units) val[u] = src[idx];
+    in[u] = idx < p.units;
+    val[u] = in[u] ? src[idx] : U{};
   }
   for (int n = 0; n < p.n_rows; ++n) {
     U* dst = reinterpret_cast<U*>(dst_layer + n * p.dst_stride_b);
 #pragma unroll
     for (int u = 0; u < kFanoutUnitsPerThread; ++u) {
-      const int64_t idx = base + static_cast<int64_t>(u) * blockDim.x;
-      if (idx < p.units) dst[idx] = val[u];
+      if (in[u]) store_nt(dst + base + static_cast<int64_t>(u) * blockDim.x, val[u]);
     }
   }
 }
