@@ -5,6 +5,7 @@
  *   - nanochat/flash_attention.py:131-177  flash_attn_with_kvcache (append + attention)
  *   - nanochat/flash_attention.py:69-102   _sdpa_attention masks (causal, sliding window, GQA)
  *   - nanochat/engine.py:123-137           KVCache.prefill (broadcast fan-out copy)
+ *   - nanochat/gpt.py:45-50, 468-472       the decode step's linear layers and logits head
  * Host code (Python, ctypes) validates shapes and dtypes, then calls these
  * functions with raw device pointers, element strides and the caller's stream.
  *
@@ -26,7 +27,7 @@
 extern "C" {
 #endif
 
-#define NC_KV_ABI_VERSION 5
+#define NC_KV_ABI_VERSION 6
 
 /* Element types (the torch dtypes the reference path uses). */
 enum nc_dtype {
@@ -222,6 +223,45 @@ typedef struct nc_qk_prologue {
 size_t nc_attn_rope_workspace_bytes(const nc_attn_args* args);
 
 int nc_attn_kvcache_rope(const nc_attn_args* args, const nc_qk_prologue* prologue, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Small-M linear layer of the decode step: y = x W^T (bias-free), for the
+ * projections nanochat runs on a (B, 1, C) activation with F.linear
+ * (nanochat/gpt.py:45-50 Linear.forward; callers gpt.py:87-89 c_q/c_k/c_v,
+ * :125 c_proj, :136-138 MLP, :469 lm_head).  x is (m, k), W is
+ * (n, k) (nn.Linear's layout), y is (m, n); m <= 64.  Accumulation is fp32
+ * with one rounding at the end (round to nearest even).  x and W have the
+ * same dtype (bf16 or fp16); y is that dtype or fp32.
+ *
+ * softcap > 0 selects the logits head of gpt.py:468-472 instead: the fp32
+ * accumulator is rounded to x's dtype (the lm_head output), widened, and
+ * y (fp32) = softcap * tanh(v * (1 / softcap)) -- the operations torch runs
+ * for `softcap * torch.tanh(logits.float() / softcap)`.  Passing n = the
+ * vocabulary size (not the padded row count of W) gives the sliced logits
+ * `[..., :vocab_size]` directly.
+ *
+ * K may be split over workgroups: nc_linear_workspace_bytes() is then
+ * non-zero, and the workspace follows the same rule as nc_attn_kvcache's
+ * (first NC_WORKSPACE_SYNC_BYTES zero before the first call, left zero by
+ * every call).  Results do not depend on the order in which workgroups run.
+ * ------------------------------------------------------------------------- */
+typedef struct nc_linear_args {
+  const void* x;                 /* (m, k), rows x_stride_m elements apart, 16-byte aligned */
+  const void* w;                 /* (n, k), rows w_stride_n elements apart, 16-byte aligned */
+  void* y;                       /* (m, n), rows y_stride_m elements apart */
+  void* workspace;
+  size_t workspace_bytes;
+  int64_t m, n, k;               /* 1 <= m <= 64; k a multiple of 8 */
+  int64_t x_stride_m, w_stride_n, y_stride_m;
+  int32_t dtype;                 /* x and w: NC_DTYPE_BF16 or NC_DTYPE_F16 */
+  int32_t y_dtype;               /* dtype, or NC_DTYPE_F32; NC_DTYPE_F32 when softcap > 0 */
+  float softcap;                 /* 0: plain linear */
+} nc_linear_args;
+
+/* Bytes of workspace nc_linear needs for these sizes (0: none). */
+size_t nc_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+int nc_linear(const nc_linear_args* args, void* stream);
 
 /* Name of an nc_status code (static string). */
 const char* nc_strerror(int status);

@@ -16,7 +16,7 @@ import torch
 # NANOCHAT_AMD_LIB points at another build of the same library (e.g. a tuning
 # variant); by default the in-tree build next to this file is loaded.
 LIB_PATH = Path(os.environ.get("NANOCHAT_AMD_LIB", Path(__file__).resolve().parent / "libnc_kv.so"))
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -88,6 +88,17 @@ class QKPrologue(ctypes.Structure):
     ]
 
 
+class LinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", _c_void_p), ("w", _c_void_p), ("y", _c_void_p),
+        ("workspace", _c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("m", _i64), ("n", _i64), ("k", _i64),
+        ("x_stride_m", _i64), ("w_stride_n", _i64), ("y_stride_m", _i64),
+        ("dtype", _i32), ("y_dtype", _i32),
+        ("softcap", ctypes.c_float),
+    ]
+
+
 # Every function include/nc_kv.h declares, with its ctypes signature.
 EXPORTS = {
     "nc_abi_version": (ctypes.c_int, []),
@@ -99,6 +110,8 @@ EXPORTS = {
     "nc_attn_kvcache": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _c_void_p]),
     "nc_attn_rope_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
     "nc_attn_kvcache_rope": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.POINTER(QKPrologue), _c_void_p]),
+    "nc_linear_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
+    "nc_linear": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _c_void_p]),
 }
 
 _lib = None

@@ -24,7 +24,7 @@ OBJ_DIR = PKG_DIR / "_build"
 ARCH = "gfx950"
 
 SOURCES = ["nc_kv_abi.hip", "kv_copy.hip", "attn_decode.hip", "attn_decode_bf16.hip", "attn_decode_f16.hip",
-           "attn_decode_f32.hip", "attn_chunk.hip"]
+           "attn_decode_f32.hip", "attn_chunk.hip", "linear_small_m.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -43,6 +43,7 @@ HIPCC_FLAGS = [
 # of 3.
 SOURCE_FLAGS = {
     "attn_chunk.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
+    "linear_small_m.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form"),
 }
 
 

@@ -417,4 +417,37 @@ int nc_attn_kvcache_rope(const nc_attn_args* args, const nc_qk_prologue* prologu
   return run_attention(b, plan, s, nullptr, hs);
 }
 
+size_t nc_linear_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  return plan_linear(m, n, k).total_bytes;
+}
+
+int nc_linear(const nc_linear_args* args, void* stream) {
+  if (args == nullptr) return NC_ERR_NULL_ARG;
+  const nc_linear_args& a = *args;
+  if (!a.x || !a.w || !a.y) return NC_ERR_NULL_ARG;
+  if (a.m <= 0 || a.m > kLinMaxM || a.n <= 0 || a.k <= 0 || a.k % 8 != 0) return NC_ERR_BAD_SHAPE;
+  if (a.n > INT32_MAX / 2 || a.k > INT32_MAX / 2) return NC_ERR_BAD_SHAPE;
+  if (a.x_stride_m >= kLinMaxStride || a.w_stride_n >= kLinMaxStride || a.k >= kLinMaxStride) {
+    return NC_ERR_BAD_SHAPE;
+  }
+  if ((a.m > 1 && (a.x_stride_m < a.k || a.y_stride_m < a.n)) || (a.n > 1 && a.w_stride_n < a.k)) {
+    return NC_ERR_BAD_SHAPE;
+  }
+  if (!(a.softcap >= 0.0f) || a.softcap > 3.0e38f) return NC_ERR_BAD_SHAPE;  // also rejects NaN
+  if (a.dtype != NC_DTYPE_BF16 && a.dtype != NC_DTYPE_F16) return NC_ERR_DTYPE;
+  if (a.y_dtype != a.dtype && a.y_dtype != NC_DTYPE_F32) return NC_ERR_DTYPE;
+  if (a.softcap > 0.0f && a.y_dtype != NC_DTYPE_F32) return NC_ERR_DTYPE;
+  if (!aligned16(a.x) || !aligned16(a.w) || (a.x_stride_m % 8) != 0 || (a.w_stride_n % 8) != 0) {
+    return NC_ERR_ALIGNMENT;
+  }
+  if ((reinterpret_cast<uintptr_t>(a.y) % dtype_bytes(a.y_dtype)) != 0) return NC_ERR_ALIGNMENT;
+  const LinearPlan pl = plan_linear(a.m, a.n, a.k);
+  if (pl.total_bytes > 0 &&
+      (a.workspace == nullptr || a.workspace_bytes < pl.total_bytes || !aligned16(a.workspace))) {
+    return NC_ERR_WORKSPACE;
+  }
+  return launch_linear(a, pl, a.workspace, static_cast<hipStream_t>(stream)) == hipSuccess ? NC_OK : NC_ERR_LAUNCH;
+}
+
 }  // extern "C"

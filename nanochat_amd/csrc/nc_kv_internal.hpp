@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "nc_kv.h"
 
 namespace nckv {
@@ -70,5 +72,36 @@ hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const
 int max_splits();
 int default_split_bytes();
 int64_t decode_grid(int64_t n_groups, int num_splits);
+
+// ---- small-M linear (linear_small_m.hip) ----
+// Columns of W per workgroup (4 waves x 16).
+constexpr int64_t kLinCols = 64;
+// Workgroups one call aims for (two per CU); the K range is split to reach it.
+#ifndef NC_LIN_TARGET_WG
+#define NC_LIN_TARGET_WG 512
+#endif
+constexpr int64_t kLinTargetWG = NC_LIN_TARGET_WG;
+// At most this many K splits (each adds a partial tile the last workgroup reads back).
+#ifndef NC_LIN_MAX_SPLITS
+#define NC_LIN_MAX_SPLITS 4
+#endif
+constexpr int64_t kLinMaxSplits = NC_LIN_MAX_SPLITS;
+// Column blocks that can take split-K tickets (one uint32 each in the sync region).
+constexpr int64_t kLinMaxTickets = NC_WORKSPACE_SYNC_BYTES / 4;
+constexpr int64_t kLinMaxM = 64;
+// Row strides (elements) the kernel's 32-bit buffer offsets cover.
+constexpr int64_t kLinMaxStride = int64_t(1) << 24;
+
+struct LinearPlan {
+  int m_tiles;            // ceil(m / 16)
+  int64_t n_blocks;       // ceil(n / 64): one column block per workgroup (per split)
+  int64_t chunks;         // ceil(k / 128)
+  int64_t chunks_per_split;
+  int64_t splits;         // > 1: partials summed by the last workgroup of a block
+  size_t part_bytes, total_bytes;
+};
+
+LinearPlan plan_linear(int64_t m, int64_t n, int64_t k);
+hipError_t launch_linear(const nc_linear_args& a, const LinearPlan& plan, void* workspace, hipStream_t stream);
 
 }  // namespace nckv

@@ -42,7 +42,8 @@ def test_header_constants_match_python_mirror():
 def test_struct_layouts_match_header_field_order():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     for cname, pystruct in (("nc_append_args", _ext.AppendArgs), ("nc_fanout_args", _ext.FanoutArgs),
-                            ("nc_attn_args", _ext.AttnArgs), ("nc_qk_prologue", _ext.QKPrologue)):
+                            ("nc_attn_args", _ext.AttnArgs), ("nc_qk_prologue", _ext.QKPrologue),
+                            ("nc_linear_args", _ext.LinearArgs)):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), text, flags=re.S).group(1)
         names = []
         for decl in body.split(";"):
@@ -151,6 +152,59 @@ def test_invalid_arguments_are_rejected_before_launch():
     assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 6  # 9 splits need a workspace
     a.keys_per_split = 100
     assert lib.nc_attn_kvcache(ctypes.byref(a), None) == 2  # not a multiple of 64
+
+
+def test_linear_plan_splits_k_to_fill_the_gpu():
+    lib = _ext.lib()
+    sync = _ext.NC_WORKSPACE_SYNC_BYTES
+    # (m, n, k) -> splits: 64-column blocks x splits reaches about 512 workgroups, with at least
+    # one 128-wide chunk of k per split and at most 4 splits; partials are 64 columns x m_tiles x
+    # 16 rows fp32 per (block, split)
+    for (m, n, k), splits in {(32, 1280, 1280): 4, (32, 1280, 5120): 4, (32, 5120, 1280): 4,
+                              (16, 1536, 6144): 4, (1, 1280, 1280): 4, (64, 1280, 1280): 4,
+                              (32, 640, 896): 4, (32, 20000, 1280): 2, (8, 64, 256): 2}.items():
+        m_tiles, n_blocks = (m + 15) // 16, (n + 63) // 64
+        assert lib.nc_linear_workspace_bytes(m, n, k) == sync + n_blocks * splits * 64 * m_tiles * 64, (m, n, k)
+    # no split: at least 512 column blocks (lm_head)
+    assert lib.nc_linear_workspace_bytes(32, 32768, 1280) == 0
+    assert lib.nc_linear_workspace_bytes(32, 65536, 2048) == 0
+    assert lib.nc_linear_workspace_bytes(0, 16, 16) == 0
+
+
+def test_linear_rejects_bad_arguments_before_launch():
+    lib = _ext.lib()
+    a = _ext.LinearArgs()
+    assert lib.nc_linear(ctypes.byref(a), None) == 1          # NULL pointers
+    fake = 1 << 20
+    a.x = a.w = a.y = fake
+    a.m, a.n, a.k = 32, 64, 128
+    a.x_stride_m, a.w_stride_n, a.y_stride_m = 128, 128, 64
+    a.dtype = a.y_dtype = 2
+    for field, bad in (("m", 65), ("m", 0), ("k", 12), ("n", 0), ("x_stride_m", 64), ("y_stride_m", 32),
+                       ("w_stride_n", 1 << 24)):
+        good = getattr(a, field)
+        setattr(a, field, bad)
+        assert lib.nc_linear(ctypes.byref(a), None) == 2, field
+        setattr(a, field, good)
+    a.dtype = a.y_dtype = 0                                    # fp32 operands are not taken
+    assert lib.nc_linear(ctypes.byref(a), None) == 3
+    a.dtype, a.y_dtype = 2, 1                                  # bf16 operands, fp16 output
+    assert lib.nc_linear(ctypes.byref(a), None) == 3
+    a.y_dtype, a.softcap = 2, 15.0                             # the logits head writes fp32
+    assert lib.nc_linear(ctypes.byref(a), None) == 3
+    a.softcap = float("nan")
+    assert lib.nc_linear(ctypes.byref(a), None) == 2
+    a.softcap = 0.0
+    a.x_stride_m = 132                                         # rows not 16-byte aligned
+    assert lib.nc_linear(ctypes.byref(a), None) == 5
+    a.x_stride_m = 128
+    a.x = fake + 8
+    assert lib.nc_linear(ctypes.byref(a), None) == 5
+    a.x = fake
+    a.n, a.k, a.w_stride_n, a.x_stride_m, a.y_stride_m = 1280, 1280, 1280, 1280, 1280
+    assert lib.nc_linear(ctypes.byref(a), None) == 6          # K split: needs a workspace
+    a.workspace, a.workspace_bytes = fake, lib.nc_linear_workspace_bytes(32, 1280, 1280) - 16
+    assert lib.nc_linear(ctypes.byref(a), None) == 6
 
 
 def test_fanout_and_append_reject_bad_arguments():
