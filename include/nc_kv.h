@@ -263,6 +263,37 @@ size_t nc_linear_workspace_bytes(int64_t m, int64_t n, int64_t k);
 
 int nc_linear(const nc_linear_args* args, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Next-token sampling, one launch for the batch (nanochat/engine.py:141-156
+ * sample_next_token, applied to the fp32 logits of gpt.py:472):
+ *   temperature == 0: argmax of each row (first maximum; NaN counts as the
+ *     maximum, as torch.argmax does);
+ *   0 < top_k < vocab: the top_k largest logits (equal values at the cut:
+ *     lower indices first), softmax of logit / temperature over them, one
+ *     categorical draw;
+ *   otherwise: softmax of logit / temperature over the whole row, one draw.
+ * The draw is the inverse CDF at uniforms[b] in [0, 1): the first category
+ * whose running sum of exp(x - max) exceeds u times the total, categories in
+ * torch.topk's order (value descending) for top-k and in index order for the
+ * whole row.  The reference draws with torch.multinomial and its generator:
+ * the distribution is the same, the stream of draws is the caller's.  NaN
+ * logits are never drawn; a row with no finite logit yields 0 and sets
+ * NC_DEVERR_SAMPLE (torch.multinomial raises for it).
+ * ------------------------------------------------------------------------- */
+#define NC_DEVERR_SAMPLE 16
+
+typedef struct nc_sample_args {
+  const float* logits;           /* (batch, vocab) fp32, rows logits_stride elements apart */
+  const float* uniforms;         /* (batch,): one draw per row (unused when temperature == 0) */
+  int64_t* out;                  /* (batch,) token ids */
+  int32_t* error_flag;           /* optional (NULL): NC_DEVERR_SAMPLE is OR-ed in */
+  int64_t batch, vocab, logits_stride;
+  float temperature;             /* >= 0 */
+  int32_t top_k;                 /* 0 or >= vocab: whole row; else at most 1024 */
+} nc_sample_args;
+
+int nc_sample(const nc_sample_args* args, void* stream);
+
 /* Name of an nc_status code (static string). */
 const char* nc_strerror(int status);
 

@@ -24,6 +24,7 @@ NC_DEVERR_OVERFLOW = 1
 NC_DEVERR_ROPE_RANGE = 2
 NC_DEVERR_BATCH_IDX = 4
 NC_DEVERR_QLEN = 8
+NC_DEVERR_SAMPLE = 16
 # leading workspace bytes holding split counters: zero before first use, left zero by every call
 NC_WORKSPACE_SYNC_BYTES = 65536
 
@@ -99,6 +100,14 @@ class LinearArgs(ctypes.Structure):
     ]
 
 
+class SampleArgs(ctypes.Structure):
+    _fields_ = [
+        ("logits", _c_void_p), ("uniforms", _c_void_p), ("out", _c_void_p), ("error_flag", _c_void_p),
+        ("batch", _i64), ("vocab", _i64), ("logits_stride", _i64),
+        ("temperature", ctypes.c_float), ("top_k", _i32),
+    ]
+
+
 # Every function include/nc_kv.h declares, with its ctypes signature.
 EXPORTS = {
     "nc_abi_version": (ctypes.c_int, []),
@@ -112,6 +121,7 @@ EXPORTS = {
     "nc_attn_kvcache_rope": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.POINTER(QKPrologue), _c_void_p]),
     "nc_linear_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),
     "nc_linear": (ctypes.c_int, [ctypes.POINTER(LinearArgs), _c_void_p]),
+    "nc_sample": (ctypes.c_int, [ctypes.POINTER(SampleArgs), _c_void_p]),
 }
 
 _lib = None

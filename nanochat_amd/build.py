@@ -24,7 +24,8 @@ OBJ_DIR = PKG_DIR / "_build"
 ARCH = "gfx950"
 
 SOURCES = ["nc_kv_abi.hip", "kv_copy.hip", "attn_decode.hip", "attn_decode_bf16.hip", "attn_decode_f16.hip",
-           "attn_decode_f32.hip", "attn_chunk.hip", "linear_small_m.hip"]
+           "attn_decode_f32.hip", "attn_chunk.hip", "linear_small_m.hip",
+           "sample.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

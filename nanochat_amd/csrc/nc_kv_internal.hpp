@@ -102,6 +102,10 @@ struct LinearPlan {
 };
 
 LinearPlan plan_linear(int64_t m, int64_t n, int64_t k);
+
+// ---- next-token sampling (sample.hip) ----
+constexpr int kMaxTopK = 1024;
+hipError_t launch_sample(const nc_sample_args& a, hipStream_t stream);
 hipError_t launch_linear(const nc_linear_args& a, const LinearPlan& plan, void* workspace, hipStream_t stream);
 
 }  // namespace nckv

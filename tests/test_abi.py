@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_header_constants_match_python_mirror():
     text = HEADER.read_text()
     for name in ("NC_KV_ABI_VERSION", "NC_WORKSPACE_SYNC_BYTES", "NC_DEVERR_OVERFLOW", "NC_DEVERR_ROPE_RANGE",
-                 "NC_DEVERR_BATCH_IDX", "NC_DEVERR_QLEN"):
+                 "NC_DEVERR_BATCH_IDX", "NC_DEVERR_QLEN", "NC_DEVERR_SAMPLE"):
         value = int(re.search(r"#define %s (\d+)" % name, text).group(1))
         py = _ext.ABI_VERSION if name == "NC_KV_ABI_VERSION" else getattr(_ext, name)
         assert py == value, name
@@ -43,7 +43,7 @@ def test_struct_layouts_match_header_field_order():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     for cname, pystruct in (("nc_append_args", _ext.AppendArgs), ("nc_fanout_args", _ext.FanoutArgs),
                             ("nc_attn_args", _ext.AttnArgs), ("nc_qk_prologue", _ext.QKPrologue),
-                            ("nc_linear_args", _ext.LinearArgs)):
+                            ("nc_linear_args", _ext.LinearArgs), ("nc_sample_args", _ext.SampleArgs)):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (cname, cname), text, flags=re.S).group(1)
         names = []
         for decl in body.split(";"):
@@ -205,6 +205,26 @@ def test_linear_rejects_bad_arguments_before_launch():
     assert lib.nc_linear(ctypes.byref(a), None) == 6          # K split: needs a workspace
     a.workspace, a.workspace_bytes = fake, lib.nc_linear_workspace_bytes(32, 1280, 1280) - 16
     assert lib.nc_linear(ctypes.byref(a), None) == 6
+
+
+def test_sample_rejects_bad_arguments_before_launch():
+    lib = _ext.lib()
+    a = _ext.SampleArgs()
+    assert lib.nc_sample(ctypes.byref(a), None) == 1           # NULL pointers
+    fake = 1 << 20
+    a.logits, a.out = fake, fake
+    a.batch, a.vocab, a.logits_stride, a.temperature, a.top_k = 4, 5000, 5000, 1.0, 0
+    assert lib.nc_sample(ctypes.byref(a), None) == 1           # sampling needs uniforms
+    a.uniforms = fake
+    for field, bad in (("batch", 0), ("vocab", 0), ("logits_stride", 4999), ("top_k", -1), ("top_k", 1025),
+                       ("temperature", -1.0), ("temperature", float("nan"))):
+        good = getattr(a, field)
+        setattr(a, field, bad)
+        assert lib.nc_sample(ctypes.byref(a), None) == 2, field
+        setattr(a, field, good)
+    a.out = fake + 4                                            # int64 ids need 8-byte alignment
+    assert lib.nc_sample(ctypes.byref(a), None) == 5
+    a.out = fake
 
 
 def test_fanout_and_append_reject_bad_arguments():
