@@ -342,10 +342,11 @@ def run_c3(dev, stream, steps, kps=0, ckps=0):
 
 def run_e2e(dev, stream, steps, kps=0, ckps=0):
     """d20 model decode step (random-init weights, bf16, SSSL windows at sequence_len 2048): B=32 rows at
-    position 1280, one token per row per step.  Three timings of GPT.forward with the cache:
-    the reference's op-by-op QK prologue (eager; it needs get_pos(), a host sync), the fused prologue
-    (eager), and the fused prologue with one decode step captured in a HIP graph (possible because the
-    fused path has no host sync)."""
+    position 1280, one token per row per step.  Timings of GPT.forward with the cache: the reference's
+    op-by-op QK prologue (eager; it needs get_pos(), a host sync), the fused prologue (eager), and the
+    fused prologue with one decode step captured in a HIP graph (possible because the fused path has no
+    host sync), with torch's logits head and with the fused one (nc_linear + softcap).  Then the
+    C3-shaped Engine.generate in the same modes, the last one also sampling with nc_sample."""
     from nanochat_amd.engine import KVCache
     from nanochat_amd.gpt import GPTConfig, build_model
     cfg = GPTConfig(sequence_len=2048, vocab_size=32768, n_layer=20, n_head=10, n_kv_head=10, n_embd=1280)
@@ -376,24 +377,29 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
             model.forward(ids, kv_cache=kv)
 
     res = {}
+    model.fused_logits_head = False
     for name, fused in (("op_by_op_eager", False), ("fused_eager", True)):
         model.fused_qk_prologue = fused
         kv.cache_seqlens.fill_(P)
         res[name] = timed(step, steps)
     model.fused_qk_prologue = True
-    kv.cache_seqlens.fill_(P)
-    with torch.cuda.stream(stream):
-        step()  # warm the workspace on this stream
-        stream.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.inference_mode(), torch.cuda.graph(graph, stream=stream):
-        model.forward(ids, kv_cache=kv)
-    kv.cache_seqlens.fill_(P)
-    res["fused_graph"] = timed(graph.replay, steps)
+    # graph-captured step with torch's logits head, then with the fused head (nc_linear + softcap)
+    for name, head in (("fused_graph_torch_head", False), ("fused_graph", True)):
+        model.fused_logits_head = head
+        kv.cache_seqlens.fill_(P)
+        with torch.cuda.stream(stream):
+            step()  # warm the workspace on this stream
+            stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.inference_mode(), torch.cuda.graph(graph, stream=stream):
+            model.forward(ids, kv_cache=kv)
+        kv.cache_seqlens.fill_(P)
+        res[name] = timed(graph.replay, steps)
+        del graph
     out = {"config": "e2e", "workload": f"d20 GPT decode step (random init, bf16, SSSL), B={B} at position {P}, "
                                         f"{steps} steps", **{k + "_ms_per_step": round(v, 4) for k, v in res.items()},
            "tokens_per_s_fused_graph": round(B / (res["fused_graph"] * 1e-3), 1)}
-    del graph, kv, model
+    del kv, model
     torch.cuda.empty_cache()
 
     # C3-shaped Engine.generate: d24, 1024-token prompt, 16 samples, `steps` tokens (wall clock, host loop included)
@@ -411,9 +417,12 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
     model3 = build_model(cfg3, dev, compute_dtype=torch.bfloat16, seed=0)
     g3 = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, 32759, (1024,), generator=g3).tolist()
-    for name, fused, use_graph in (("op_by_op", False, False), ("fused", True, False), ("fused_graph", True, True)):
+    for name, fused, use_graph, head_smp in (("op_by_op", False, False, False), ("fused", True, False, False),
+                                             ("fused_graph", True, True, False),
+                                             ("fused_graph_head_sampler", True, True, True)):
         model3.fused_qk_prologue = fused
-        engine = Engine(model3, _Tok(), use_graph=use_graph)
+        model3.fused_logits_head = head_smp
+        engine = Engine(model3, _Tok(), use_graph=use_graph, fused_sampling=head_smp)
         for _ in engine.generate(prompt, num_samples=16, max_tokens=4, temperature=1.0, seed=0):
             pass  # warm up
         torch.cuda.synchronize()
@@ -426,6 +435,7 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
         out[f"engine_c3_{name}_ms_per_step"] = round(dt * 1e3 / n, 4)
         out[f"engine_c3_{name}_tokens_per_s"] = round(16 * n / dt, 1)
     model3.fused_qk_prologue = True
+    model3.fused_logits_head = True
     out["engine_c3_workload"] = (f"Engine.generate d24 (random init, bf16), 1024-token prompt, 16 samples, {steps} "
                                  "tokens incl. prefill + fan-out; wall clock")
     return out

@@ -283,7 +283,7 @@ int nc_linear(const nc_linear_args* args, void* stream);
 #define NC_DEVERR_SAMPLE 16
 
 typedef struct nc_sample_args {
-  const float* logits;           /* (batch, vocab) fp32, rows logits_stride elements apart */
+  const float* logits;           /* (batch, vocab) fp32, rows logits_stride elements apart (0: one row for all) */
   const float* uniforms;         /* (batch,): one draw per row (unused when temperature == 0) */
   int64_t* out;                  /* (batch,) token ids */
   int32_t* error_flag;           /* optional (NULL): NC_DEVERR_SAMPLE is OR-ed in */

@@ -455,7 +455,10 @@ int nc_sample(const nc_sample_args* args, void* stream) {
   const nc_sample_args& a = *args;
   if (!a.logits || !a.out || (a.temperature > 0.0f && !a.uniforms)) return NC_ERR_NULL_ARG;
   if (a.batch <= 0 || a.batch > INT32_MAX || a.vocab <= 0 || a.vocab > INT32_MAX / 2) return NC_ERR_BAD_SHAPE;
-  if (a.batch > 1 && a.logits_stride < a.vocab) return NC_ERR_BAD_SHAPE;
+  // rows logits_stride apart; 0 broadcasts one row to the batch (an expanded tensor)
+  if (a.logits_stride < 0 || (a.batch > 1 && a.logits_stride != 0 && a.logits_stride < a.vocab)) {
+    return NC_ERR_BAD_SHAPE;
+  }
   if (!(a.temperature >= 0.0f) || a.temperature > 3.0e38f) return NC_ERR_BAD_SHAPE;   // also NaN
   if (a.top_k < 0 || (a.top_k > kMaxTopK && a.top_k < a.vocab)) return NC_ERR_BAD_SHAPE;
   if ((reinterpret_cast<uintptr_t>(a.logits) & 3u) != 0 || (reinterpret_cast<uintptr_t>(a.out) & 7u) != 0) {

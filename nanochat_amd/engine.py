@@ -23,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _ext
+from . import sampling as gpu_sampling
 
 
 class KVCache:
@@ -222,11 +223,15 @@ class GraphDecodeStep:
 class Engine:
     """Batched generation with one prefill and a fanned-out KV cache."""
 
-    def __init__(self, model, tokenizer, use_graph=None):
+    def __init__(self, model, tokenizer, use_graph=None, fused_sampling=None):
         self.model = model
         self.tokenizer = tokenizer
         # None: replay decode steps from a HIP graph whenever the model runs the fused QK prologue on the GPU
         self.use_graph = use_graph
+        # None: sample with the HIP kernel (nc_sample) on the GPU.  Same distribution as the
+        # reference's torch.multinomial, one torch.rand draw per row from the same generator;
+        # greedy decoding gives the same tokens either way.  False keeps the torch ops.
+        self.fused_sampling = fused_sampling
 
     def _graph_decode(self, device):
         if device.type != "cuda" or not getattr(self.model, "fused_qk_prologue", False):
@@ -260,6 +265,8 @@ class Engine:
         del prefill_cache
 
         step = GraphDecodeStep(self.model, cache, num_samples, device) if self._graph_decode(device) else None
+        fused = device.type == "cuda" and self.fused_sampling is not False
+        sampler = gpu_sampling.sample_next_token if fused else sample_next_token
         rows = [RowState(tokens.copy()) for _ in range(num_samples)]
         generated = 0
         while True:
@@ -267,7 +274,7 @@ class Engine:
                 break
             if all(r.completed for r in rows):
                 break
-            sampled = sample_next_token(logits, rng, temperature, top_k)[:, 0].tolist()
+            sampled = sampler(logits, rng, temperature, top_k)[:, 0].tolist()
             column, masks = [], []
             for i, r in enumerate(rows):
                 forced = len(r.forced_tokens) > 0

@@ -28,6 +28,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import linear as head_kernel
 from .common import COMPUTE_DTYPE
 from .flash_attention import flash_attn
 
@@ -56,15 +57,19 @@ class CastLinear(nn.Linear):
     re-reading the fp32 weights each decode step.
     """
 
-    def forward(self, x):
-        if torch.is_grad_enabled() or self.weight.dtype == x.dtype:
-            return F.linear(x, self.weight.to(dtype=x.dtype))
-        key = (x.dtype, self.weight._version, self.weight.data_ptr())
+    def weight_as(self, dtype):
+        """The weight in `dtype` (kept between calls when autograd is off)."""
+        if torch.is_grad_enabled() or self.weight.dtype == dtype:
+            return self.weight.to(dtype=dtype)
+        key = (dtype, self.weight._version, self.weight.data_ptr())
         cached = getattr(self, "_cast", None)
         if cached is None or cached[0] != key:
-            cached = (key, self.weight.to(dtype=x.dtype))
+            cached = (key, self.weight.to(dtype=dtype))
             self._cast = cached
-        return F.linear(x, cached[1])
+        return cached[1]
+
+    def forward(self, x):
+        return F.linear(x, self.weight_as(x.dtype))
 
 
 def carries_value_embedding(layer, n_layer):
@@ -256,6 +261,11 @@ class GPT(nn.Module):
     # cache_seqlens: no get_pos() host sync and ~10 fewer launches per layer.  False
     # keeps the reference's op-by-op sequence.
     fused_qk_prologue = True
+    # Decode-sized logits heads (CUDA, bf16/fp16, at most 64 rows) run lm_head, the vocabulary
+    # slice, the fp32 cast and the softcap as one kernel (nanochat_amd.linear.logits_head).  The
+    # logits are the same up to the GEMM's summation order (bf16-rounded as the reference's);
+    # False keeps F.linear and torch's softcap.
+    fused_logits_head = True
 
     def forward(self, idx, kv_cache=None):
         """Logits (B, T, vocab) in fp32.  With a cache, attention appends into it."""
@@ -303,6 +313,10 @@ class GPT(nn.Module):
             x = x - self.backout_lambda.to(x.dtype) * x_backout
         x = rms(x)
         softcap = 15
+        if self.fused_logits_head and x.is_cuda:
+            w = self.lm_head.weight_as(x.dtype)
+            if head_kernel.supported(x, w):
+                return head_kernel.logits_head(x, w, self.config.vocab_size, softcap)
         logits = self.lm_head(x)[..., :self.config.vocab_size].float()
         return softcap * torch.tanh(logits / softcap)
 

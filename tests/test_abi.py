@@ -216,7 +216,8 @@ def test_sample_rejects_bad_arguments_before_launch():
     a.batch, a.vocab, a.logits_stride, a.temperature, a.top_k = 4, 5000, 5000, 1.0, 0
     assert lib.nc_sample(ctypes.byref(a), None) == 1           # sampling needs uniforms
     a.uniforms = fake
-    for field, bad in (("batch", 0), ("vocab", 0), ("logits_stride", 4999), ("top_k", -1), ("top_k", 1025),
+    for field, bad in (("batch", 0), ("vocab", 0), ("logits_stride", 4999), ("logits_stride", -1), ("top_k", -1),
+                       ("top_k", 1025),
                        ("temperature", -1.0), ("temperature", float("nan"))):
         good = getattr(a, field)
         setattr(a, field, bad)

@@ -244,3 +244,42 @@ def test_graph_replayed_decode_steps_equal_eager_steps(temperature):
         runs.append([col for col, _ in engine.generate(GOLDEN["prompt"], num_samples=4, max_tokens=24,
                                                        temperature=temperature, seed=7)])
     assert runs[0] == runs[1]
+
+
+# ---- the fused logits head and the fused sampler in the model and engine ----
+def test_fused_logits_head_in_the_model():
+    """A bf16 decode step: logits from the fused head (lm_head + slice + fp32 + softcap in one kernel)
+    equal the reference's F.linear + torch softcap up to the GEMM's summation order (one bf16 rounding
+    of the pre-softcap logits either way)."""
+    cfg = gpt.GPTConfig(sequence_len=256, vocab_size=5000, n_layer=2, n_head=4, n_kv_head=4, n_embd=256)
+    model = gpt.build_model(cfg, DEV, compute_dtype=torch.bfloat16, seed=3)
+    torch.nn.init.normal_(model.lm_head.weight, std=0.05)     # logits of a few units: softcap's curved range
+    g = torch.Generator().manual_seed(3)
+    prompt = torch.randint(0, 5000, (1, 40), generator=g).to(DEV)
+    step_ids = torch.randint(0, 5000, (8, 1), generator=g).to(DEV)
+    outs = []
+    for fused in (True, False):
+        model.fused_logits_head = fused
+        kv = KVCache(batch_size=8, num_heads=4, seq_len=64, head_dim=64, num_layers=2, device=DEV,
+                     dtype=torch.bfloat16)
+        pre = KVCache(batch_size=1, num_heads=4, seq_len=40, head_dim=64, num_layers=2, device=DEV,
+                      dtype=torch.bfloat16)
+        with torch.inference_mode():
+            model.forward(prompt, kv_cache=pre)
+            kv.prefill(pre)
+            outs.append(model.forward(step_ids, kv_cache=kv)[:, -1, :].float())
+    model.fused_logits_head = True
+    a, b = outs
+    assert a.shape == (8, 5000)
+    assert float((a - b).abs().max()) <= 1e-2 * float(b.abs().max()) + 1e-3
+    assert float((a.argmax(-1) == b.argmax(-1)).float().mean()) >= 0.75
+
+
+def test_engine_fused_sampler_greedy_equals_torch_sampler():
+    model = c1_model("perturbed").to(DEV)
+    runs = []
+    for fused in (True, False):
+        engine = Engine(model, SpecialTokens(), fused_sampling=fused)
+        runs.append([col for col, _ in engine.generate(GOLDEN["prompt"], num_samples=4, max_tokens=16,
+                                                       temperature=0.0, seed=7)])
+    assert runs[0] == runs[1]

@@ -130,6 +130,15 @@ def test_nan_never_drawn_and_all_inf_row_flags():
     assert _ext.read_and_clear_device_errors(xd.device) & _ext.NC_DEVERR_SAMPLE
 
 
+def test_expanded_logits_broadcast_one_row():
+    row = _logits(11, 1, 32768)
+    x = row.to(DEV).expand(16, -1)                 # row stride 0, as Engine.generate's first step
+    u = torch.rand(16, generator=gen(11))
+    got = sample_with_uniforms(x, u.to(DEV), 1.0, 50).cpu()[:, 0]
+    want = sample_with_uniforms(x.contiguous(), u.to(DEV), 1.0, 50).cpu()[:, 0]
+    assert torch.equal(got, want)
+
+
 def test_sample_next_token_api_and_graph_replay():
     x = _logits(9, 16, 32768).to(DEV)
     rng = torch.Generator(device=DEV)
