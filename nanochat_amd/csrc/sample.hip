@@ -31,7 +31,7 @@ namespace nckv {
 
 namespace {
 
-constexpr int kSmpThreads = 512;
+constexpr int kSmpThreads = 1024;
 constexpr int kSmpWaves = kSmpThreads / kWave;
 
 struct SampleParams {
@@ -63,6 +63,64 @@ struct SmpShared {
   uint32_t u[kSmpWaves];
 };
 
+// f(i, v) for every element of the row, threads striding over 16-byte groups
+// (coalesced), 4 groups in flight per thread; each thread sees its indices in
+// increasing order.
+template <typename F>
+__device__ __forceinline__ void for_strided(const float* row, int vocab, F f) {
+  int tail = 0;
+  if ((reinterpret_cast<uintptr_t>(row) & 15u) == 0) {
+    const int n4 = vocab / 4;
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    int g = threadIdx.x;
+    for (; g + 3 * kSmpThreads < n4; g += 4 * kSmpThreads) {
+      float4 a[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = r4[g + u * kSmpThreads];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int b = 4 * (g + u * kSmpThreads);
+        f(b, a[u].x); f(b + 1, a[u].y); f(b + 2, a[u].z); f(b + 3, a[u].w);
+      }
+    }
+    for (; g < n4; g += kSmpThreads) {
+      const float4 a = r4[g];
+      f(4 * g, a.x); f(4 * g + 1, a.y); f(4 * g + 2, a.z); f(4 * g + 3, a.w);
+    }
+    tail = 4 * n4;
+  }
+  for (int j = tail + static_cast<int>(threadIdx.x); j < vocab; j += kSmpThreads) f(j, row[j]);
+}
+
+// f(i, v) for i in [i0, i1) in order, with 16-byte loads where aligned.
+template <typename F>
+__device__ __forceinline__ void for_segment(const float* row, int i0, int i1, F f) {
+  int i = i0;
+  if ((reinterpret_cast<uintptr_t>(row + i0) & 15u) == 0) {
+    for (; i + 16 <= i1; i += 16) {
+      float4 a[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = *reinterpret_cast<const float4*>(row + i + 4 * u);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        f(i + 4 * u, a[u].x); f(i + 4 * u + 1, a[u].y); f(i + 4 * u + 2, a[u].z); f(i + 4 * u + 3, a[u].w);
+      }
+    }
+    for (; i + 4 <= i1; i += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(row + i);
+      f(i, a.x); f(i + 1, a.y); f(i + 2, a.z); f(i + 3, a.w);
+    }
+  }
+  for (; i < i1; ++i) f(i, row[i]);
+}
+
+// Thread t's contiguous segment of the row (a multiple of 4 elements long).
+__device__ __forceinline__ void row_segment(int vocab, int& i0, int& i1) {
+  const int seg = (((vocab + kSmpThreads - 1) / kSmpThreads) + 3) & ~3;
+  i0 = min(vocab, static_cast<int>(threadIdx.x) * seg);
+  i1 = min(vocab, i0 + seg);
+}
+
 // Exclusive prefix sum over the block's threads (thread order), and the total.
 template <typename T>
 __device__ T block_exclusive_scan(T v, T* wave_tot, T& total) {
@@ -91,13 +149,12 @@ __device__ void row_argmax(const float* row, int vocab, int64_t* out, SmpShared&
   float best = -INFINITY;
   int bi = INT32_MAX;
   bool bnan = false;
-  for (int i = threadIdx.x; i < vocab; i += kSmpThreads) {
-    const float v = row[i];
+  for_strided(row, vocab, [&](int i, float v) __attribute__((always_inline)) {
     const bool nan = v != v;
     // strictly larger (NaN above everything) replaces; ties keep the earlier index
     const bool take = bi == INT32_MAX || (nan && !bnan) || (!bnan && !nan && v > best);
     if (take) { best = v; bi = i; bnan = nan; }
-  }
+  });
   // wave reduce on (nan, value, -index)
 #pragma unroll
   for (int o = kWave / 2; o > 0; o /= 2) {
@@ -140,10 +197,10 @@ __device__ __forceinline__ float finite_or_neg_inf(float v) { return v != v ? -I
 __device__ void row_sample_full(const SampleParams& p, const float* row, float u, int64_t* out, SmpShared& sh,
                                 float* scan_tmp, int* pick) {
   const int vocab = p.vocab;
-  const int seg = (vocab + kSmpThreads - 1) / kSmpThreads;
-  const int i0 = min(vocab, static_cast<int>(threadIdx.x) * seg), i1 = min(vocab, i0 + seg);
+  int i0, i1;
+  row_segment(vocab, i0, i1);
   float mx = -INFINITY;
-  for (int i = threadIdx.x; i < vocab; i += kSmpThreads) mx = fmaxf(mx, finite_or_neg_inf(row[i]) * p.inv_temp);
+  for_strided(row, vocab, [&](int, float v) __attribute__((always_inline)) { mx = fmaxf(mx, finite_or_neg_inf(v) * p.inv_temp); });
   // block max
 #pragma unroll
   for (int o = kWave / 2; o > 0; o /= 2) mx = fmaxf(mx, __shfl_xor(mx, o));
@@ -162,11 +219,11 @@ __device__ void row_sample_full(const SampleParams& p, const float* row, float u
   }
   float local = 0.0f;
   int last_pos = -1;
-  for (int i = i0; i < i1; ++i) {
-    const float e = expf(finite_or_neg_inf(row[i]) * p.inv_temp - rmax);
+  for_segment(row, i0, i1, [&](int i, float v) __attribute__((always_inline)) {
+    const float e = expf(finite_or_neg_inf(v) * p.inv_temp - rmax);
     local += e;
     if (e > 0.0f) last_pos = i;
-  }
+  });
   float total;
   const float excl = block_exclusive_scan<float>(local, scan_tmp, total);
   const float target = u * total;
@@ -204,10 +261,10 @@ __device__ void row_sample_topk(const SampleParams& p, const float* row, float u
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int b = threadIdx.x; b < 256; b += kSmpThreads) hist[b] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < vocab; i += kSmpThreads) {
-      const uint32_t key = order_key(row[i]);
+    for_strided(row, vocab, [&](int, float v) __attribute__((always_inline)) {
+      const uint32_t key = order_key(v);
       if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-    }
+    });
     __syncthreads();
     if (threadIdx.x == 0) {
       int above = 0, b = 255;
@@ -226,26 +283,27 @@ __device__ void row_sample_topk(const SampleParams& p, const float* row, float u
   }
   const uint32_t kth = prefix;   // candidates: keys > kth, then the first `remaining` keys == kth
   // ---- compact the k candidates in index order (contiguous per-thread segments) ----
-  const int seg = (vocab + kSmpThreads - 1) / kSmpThreads;
-  const int i0 = min(vocab, static_cast<int>(threadIdx.x) * seg), i1 = min(vocab, i0 + seg);
+  int i0, i1;
+  row_segment(vocab, i0, i1);
   int n_gt = 0, n_eq = 0;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = order_key(row[i]);
+  for_segment(row, i0, i1, [&](int, float v) __attribute__((always_inline)) {
+    const uint32_t key = order_key(v);
     n_gt += key > kth;
     n_eq += key == kth;
-  }
+  });
   int tot_gt, tot_eq;
   int* wt = reinterpret_cast<int*>(scan_tmp);
   int o_gt = block_exclusive_scan<int>(n_gt, wt, tot_gt);
   int o_eq = block_exclusive_scan<int>(n_eq, wt, tot_eq);
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t key = order_key(row[i]);
-    if (key > kth) {
-      ckey[o_gt] = key; cidx[o_gt] = i; ++o_gt;
-    } else if (key == kth) {
-      if (o_eq < remaining) { ckey[tot_gt + o_eq] = key; cidx[tot_gt + o_eq] = i; }
-      ++o_eq;
-    }
+  if (n_gt + n_eq > 0) {
+    for_segment(row, i0, i1, [&](int i, float v) __attribute__((always_inline)) {
+      const uint32_t key = order_key(v);
+      const bool gt = key > kth, eq = key == kth;
+      if (gt) { ckey[o_gt] = key; cidx[o_gt] = i; }
+      if (eq && o_eq < remaining) { ckey[tot_gt + o_eq] = key; cidx[tot_gt + o_eq] = i; }
+      o_gt += gt;
+      o_eq += eq;
+    });
   }
   // pad to a power of two with entries that sort last
   int np2 = 1;
@@ -292,13 +350,11 @@ __device__ void row_sample_topk(const SampleParams& p, const float* row, float u
   const float target = u * total;
   if (threadIdx.x == 0) misc[2] = INT32_MAX;
   __syncthreads();
-  float run = excl;
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int j = 2 * static_cast<int>(threadIdx.x) + q;
-    run += e[q];
-    if (j < k && e[q] > 0.0f && run > target) { atomicMin(&misc[2], j); break; }
-  }
+  const int j0 = 2 * static_cast<int>(threadIdx.x);
+  const float run0 = excl + e[0], run1 = run0 + e[1];
+  const int found = (j0 < k && e[0] > 0.0f && run0 > target) ? j0
+                  : ((j0 + 1 < k && e[1] > 0.0f && run1 > target) ? j0 + 1 : INT32_MAX);
+  if (found != INT32_MAX) atomicMin(&misc[2], found);
   __syncthreads();
   if (threadIdx.x == 0) {
     int j = misc[2];
