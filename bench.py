@@ -441,6 +441,69 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
     return out
 
 
+def run_head(dev, stream, steps, kps=0, ckps=0):
+    """The decode step's tail on d20 shapes (B=32, 1280 -> 32768 vocab, bf16 weights): the logits head
+    (lm_head + slice + fp32 + softcap 15, gpt.py:468-472) as one nc_linear call against F.linear + torch's
+    ops, and next-token sampling (engine.py:141-156) as one nc_sample call against torch's ops, for greedy,
+    whole-row and top-50 draws.  Each leg is captured `steps` times in a HIP graph; us per call."""
+    import torch.nn.functional as F
+    from nanochat_amd.linear import linear, logits_head
+    from nanochat_amd.sampling import sample_with_uniforms
+    B, C, V = 32, 1280, 32768
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+
+    def timed(fn):
+        with torch.cuda.stream(stream):
+            fn()
+            stream.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for _ in range(steps):
+                    fn()
+            graph.replay()
+            stream.synchronize()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            for _ in range(4):
+                graph.replay()
+            ev1.record(stream)
+            stream.synchronize()
+            return round(ev0.elapsed_time(ev1) * 1e3 / (4 * steps), 2)
+
+    with torch.cuda.stream(stream), torch.inference_mode():
+        x = torch.randn(B, 1, C, device=dev, generator=g).bfloat16()
+        w = (torch.randn(V, C, device=dev, generator=g) * 0.05).bfloat16()
+        logits = logits_head(x, w, V, 15.0)[:, 0, :].contiguous()
+        u = torch.rand(B, device=dev, generator=g)
+
+        def torch_head():
+            lg = F.linear(x, w)[..., :V].float()
+            return 15 * torch.tanh(lg / 15)
+
+        def torch_top50():
+            vals, idx = torch.topk(logits, 50, dim=-1)
+            return idx.gather(1, torch.multinomial(F.softmax(vals / 0.8, dim=-1), 1))
+
+        res = {
+            "fused_head_us": timed(lambda: logits_head(x, w, V, 15.0)),
+            "torch_head_us": timed(torch_head),
+            "nc_linear_us": timed(lambda: linear(x, w)),
+            "torch_linear_us": timed(lambda: F.linear(x, w)),
+            "nc_greedy_us": timed(lambda: sample_with_uniforms(logits, None, 0.0)),
+            "torch_greedy_us": timed(lambda: torch.argmax(logits, dim=-1, keepdim=True)),
+            "nc_whole_row_us": timed(lambda: sample_with_uniforms(logits, u, 0.8)),
+            "torch_whole_row_us": timed(lambda: torch.multinomial(F.softmax(logits / 0.8, dim=-1), 1)),
+            "nc_top50_us": timed(lambda: sample_with_uniforms(logits, u, 0.8, 50)),
+            "torch_top50_us": timed(torch_top50),
+        }
+    head_bytes = V * C * 2 + B * C * 2 + B * V * 4
+    return {"config": "head", "workload": f"d20 logits head and sampler, B={B}, vocab {V}, K={C}, bf16; "
+                                          f"{steps} calls per graph", **res,
+            "fused_head_bytes_per_call": head_bytes,
+            "fused_head_TBps": round(head_bytes / (res["fused_head_us"] * 1e-6) / 1e12, 3)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -452,9 +515,9 @@ def main() -> int:
     ap.add_argument("--chunk-keys-per-split", type=int, default=0,
                     help="c3/c5 chunk-kernel split size (0 = library default)")
     ap.add_argument("--eager", action="store_true", help="also time the steps without a graph")
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "e2e"],
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "e2e", "head"],
                     help="c2 (default) is the metric line; c3/c4/c5 print per-phase figures; e2e times the d20 "
-                         "model's decode step")
+                         "model's decode step; head the fused logits head and the sampler")
     ap.add_argument("--rope", action="store_true",
                     help="c2 through flash_attn_with_kvcache_rope (QK prologue fused; same bytes + tables)")
     args = ap.parse_args()
@@ -469,9 +532,9 @@ def main() -> int:
         dev = torch.device("cuda", 0)
         torch.cuda.set_device(dev)
         stream = torch.cuda.Stream(device=dev)
-        runner = {"c3": run_c3, "c4": run_c4, "c5": run_c5, "e2e": run_e2e}[args.config]
+        runner = {"c3": run_c3, "c4": run_c4, "c5": run_c5, "e2e": run_e2e, "head": run_head}[args.config]
         steps = {"c3": min(args.steps, 128), "c4": min(args.steps, 256), "c5": min(args.steps, 16),
-                 "e2e": min(args.steps, 64)}[args.config]
+                 "e2e": min(args.steps, 64), "head": min(args.steps, 50)}[args.config]
         print(json.dumps(runner(dev, stream, steps, kps=args.keys_per_split, ckps=args.chunk_keys_per_split)),
               flush=True)
         return 0
