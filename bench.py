@@ -383,8 +383,11 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
         kv.cache_seqlens.fill_(P)
         res[name] = timed(step, steps)
     model.fused_qk_prologue = True
-    # graph-captured step with torch's logits head, then with the fused head (nc_linear + softcap)
-    for name, head in (("fused_graph_torch_head", False), ("fused_graph", True)):
+    # graph-captured step: separate q/k/v GEMMs and torch's logits head; one qkv GEMM; and with the
+    # fused head (nc_linear + softcap) as well
+    for name, qkv, head in (("fused_graph_torch_head", False, False), ("fused_graph_qkv", True, False),
+                            ("fused_graph", True, True)):
+        model.fused_qkv_projection = qkv
         model.fused_logits_head = head
         kv.cache_seqlens.fill_(P)
         with torch.cuda.stream(stream):

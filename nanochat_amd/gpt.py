@@ -106,9 +106,14 @@ def window_sizes(config: GPTConfig):
 
 
 class FusedRope(NamedTuple):
-    """Whole rotary tables handed to attention when the QK prologue runs inside the cache call."""
+    """Whole rotary tables handed to attention when the QK prologue runs inside the cache call.
+
+    fuse_qkv: bf16/fp16 layers compute q, k and v with one GEMM against the concatenated
+    c_q/c_k/c_v weights; q, k, v are strided views of its output (the cache call takes them as is).
+    """
     cos: torch.Tensor
     sin: torch.Tensor
+    fuse_qkv: bool = False
 
 
 class CausalSelfAttention(nn.Module):
@@ -128,11 +133,28 @@ class CausalSelfAttention(nn.Module):
         self.ve_gate = (CastLinear(self.ve_gate_channels, self.n_kv_head, bias=False)
                         if carries_value_embedding(layer_idx, config.n_layer) else None)
 
+    def qkv_weight(self, dtype):
+        """cat(c_q, c_k, c_v) weights in `dtype` (kept between calls while the weights are unchanged)."""
+        mods = (self.c_q, self.c_k, self.c_v)
+        key = (dtype,) + tuple((m.weight.data_ptr(), m.weight._version) for m in mods)
+        cached = getattr(self, "_qkv", None)
+        if torch.is_grad_enabled() or cached is None or cached[0] != key:
+            cached = (key, torch.cat([m.weight_as(dtype) for m in mods], dim=0))
+            self._qkv = cached
+        return cached[1]
+
     def forward(self, x, ve, cos_sin, window_size, kv_cache):
         B, T, _ = x.size()
-        q = self.c_q(x).view(B, T, self.n_head, self.head_dim)
-        k = self.c_k(x).view(B, T, self.n_kv_head, self.head_dim)
-        v = self.c_v(x).view(B, T, self.n_kv_head, self.head_dim)
+        if isinstance(cos_sin, FusedRope) and cos_sin.fuse_qkv and x.dtype in (torch.bfloat16, torch.float16):
+            qkv = F.linear(x, self.qkv_weight(x.dtype))
+            nq, nk = self.n_head * self.head_dim, self.n_kv_head * self.head_dim
+            q = qkv[..., :nq].view(B, T, self.n_head, self.head_dim)
+            k = qkv[..., nq:nq + nk].view(B, T, self.n_kv_head, self.head_dim)
+            v = qkv[..., nq + nk:].view(B, T, self.n_kv_head, self.head_dim)
+        else:
+            q = self.c_q(x).view(B, T, self.n_head, self.head_dim)
+            k = self.c_k(x).view(B, T, self.n_kv_head, self.head_dim)
+            v = self.c_v(x).view(B, T, self.n_kv_head, self.head_dim)
         if ve is not None:
             ve = ve.view(B, T, self.n_kv_head, self.head_dim)
             gate = 3 * torch.sigmoid(self.ve_gate(x[..., :self.ve_gate_channels]))
@@ -266,13 +288,17 @@ class GPT(nn.Module):
     # logits are the same up to the GEMM's summation order (bf16-rounded as the reference's);
     # False keeps F.linear and torch's softcap.
     fused_logits_head = True
+    # With the fused QK prologue, bf16/fp16 attention layers compute q, k, v with one GEMM (three
+    # launches become one); False keeps c_q, c_k, c_v as separate F.linear calls.
+    fused_qkv_projection = True
 
     def forward(self, idx, kv_cache=None):
         """Logits (B, T, vocab) in fp32.  With a cache, attention appends into it."""
         B, T = idx.size()
         assert T <= self.cos.size(1), f"Sequence length grew beyond the rotary table: {T} > {self.cos.size(1)}"
         if kv_cache is not None and self.fused_qk_prologue and idx.is_cuda:
-            cos_sin = FusedRope(self.cos, self.sin)  # positions beyond the table set a device flag
+            # positions beyond the table set a device flag
+            cos_sin = FusedRope(self.cos, self.sin, self.fused_qkv_projection)
         else:
             T0 = 0 if kv_cache is None else kv_cache.get_pos()
             cos_sin = self.cos[:, T0:T0 + T], self.sin[:, T0:T0 + T]

@@ -283,3 +283,32 @@ def test_engine_fused_sampler_greedy_equals_torch_sampler():
         runs.append([col for col, _ in engine.generate(GOLDEN["prompt"], num_samples=4, max_tokens=16,
                                                        temperature=0.0, seed=7)])
     assert runs[0] == runs[1]
+
+
+def test_fused_qkv_projection_in_the_model():
+    """A bf16 decode step with q, k, v as views of one GEMM (fused_qkv_projection) equals the three
+    separate projections up to the GEMM's summation order, logits and appended cache."""
+    cfg = gpt.GPTConfig(sequence_len=256, vocab_size=5000, n_layer=3, n_head=4, n_kv_head=2, n_embd=256)
+    model = gpt.build_model(cfg, DEV, compute_dtype=torch.bfloat16, seed=4)
+    for blk in model.transformer.h:
+        torch.nn.init.normal_(blk.attn.c_proj.weight, std=0.02)
+    g = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, 5000, (1, 24), generator=g).to(DEV)
+    step_ids = torch.randint(0, 5000, (4, 1), generator=g).to(DEV)
+    outs = []
+    for fused in (True, False):
+        model.fused_qkv_projection = fused
+        kv = KVCache(batch_size=4, num_heads=2, seq_len=40, head_dim=64, num_layers=3, device=DEV,
+                     dtype=torch.bfloat16)
+        pre = KVCache(batch_size=1, num_heads=2, seq_len=24, head_dim=64, num_layers=3, device=DEV,
+                      dtype=torch.bfloat16)
+        with torch.inference_mode():
+            model.forward(prompt, kv_cache=pre)
+            kv.prefill(pre)
+            logits = [model.forward(step_ids, kv_cache=kv)[:, -1, :].float() for _ in range(2)]
+        outs.append((logits, kv))
+    model.fused_qkv_projection = True
+    for a, b in zip(outs[0][0], outs[1][0]):
+        assert float((a - b).abs().max()) <= 2e-2 * float(b.abs().max()) + 1e-3
+    assert torch.equal(outs[0][1].cache_seqlens, outs[1][1].cache_seqlens)
+    assert float((outs[0][1].k_cache.float() - outs[1][1].k_cache.float()).abs().max()) <= 0.05
