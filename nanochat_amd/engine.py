@@ -228,9 +228,9 @@ class Engine:
         self.tokenizer = tokenizer
         # None: replay decode steps from a HIP graph whenever the model runs the fused QK prologue on the GPU
         self.use_graph = use_graph
-        # None: sample with the HIP kernel (nc_sample) on the GPU.  Same distribution as the
-        # reference's torch.multinomial, one torch.rand draw per row from the same generator;
-        # greedy decoding gives the same tokens either way.  False keeps the torch ops.
+        # None: sample with the HIP kernel (nc_sample) on the GPU (top_k up to 1024).  Same
+        # distribution as the reference's torch.multinomial, one torch.rand draw per row from the
+        # same generator; greedy decoding gives the same tokens either way.  False keeps the torch ops.
         self.fused_sampling = fused_sampling
 
     def _graph_decode(self, device):
@@ -265,7 +265,8 @@ class Engine:
         del prefill_cache
 
         step = GraphDecodeStep(self.model, cache, num_samples, device) if self._graph_decode(device) else None
-        fused = device.type == "cuda" and self.fused_sampling is not False
+        fused = (device.type == "cuda" and self.fused_sampling is not False
+                 and (top_k is None or top_k <= gpu_sampling.MAX_TOP_K))   # larger top_k: torch's ops
         sampler = gpu_sampling.sample_next_token if fused else sample_next_token
         rows = [RowState(tokens.copy()) for _ in range(num_samples)]
         generated = 0

@@ -55,7 +55,8 @@ def _compare_draws(x, u, T, top_k):
     assert compared >= 0.75 * x.shape[0]
 
 
-@pytest.mark.parametrize("V,k,T", [(32768, None, 1.0), (50257, None, 0.7), (32768, 200, 1.0), (32768, 1024, 1.5)])
+@pytest.mark.parametrize("V,k,T", [(32768, None, 1.0), (50257, None, 0.7), (32768, 200, 1.0), (32768, 1024, 1.5),
+                                   (65536, 100, 0.9)])
 def test_draws_at_category_midpoints_pick_that_category(V, k, T):
     # u at the middle of a chosen category's CDF interval (float64): the kernel must return it
     x = _logits(30 + V, 32, V)
@@ -83,17 +84,18 @@ def test_whole_row_draws_match_oracle(V, T):
 
 
 @pytest.mark.parametrize("V,k,T", [(32768, 1, 1.0), (32768, 5, 1.0), (32768, 50, 0.7), (32768, 200, 1.0),
-                                   (32768, 1024, 1.3), (1000, 999, 1.0), (300, 64, 0.9)])
+                                   (32768, 1024, 1.3), (1000, 999, 1.0), (300, 64, 0.9), (50257, 50, 1.0),
+                                   (65536, 1024, 0.8)])
 def test_top_k_draws_match_oracle(V, k, T):
     x = _logits(20 + k, 40, V)
     u = torch.rand(40, generator=gen(k))
     _compare_draws(x, u, T, k)
 
 
-def test_top_k_ties_at_the_cut_keep_lower_indices():
-    V = 4096
+@pytest.mark.parametrize("V", [4096, 40000])
+def test_top_k_ties_at_the_cut_keep_lower_indices(V):
     x = torch.zeros(64, V)
-    x[:, [5, 700, 701, 3000, 4095]] = 2.0           # 5 equal maxima, k = 3: indices 5, 700, 701
+    x[:, [5, 700, 701, 3000, V - 1]] = 2.0          # 5 equal maxima, k = 3: indices 5, 700, 701
     u = (torch.arange(64, dtype=torch.float32) + 0.5) / 64
     got = sample_with_uniforms(x.to(DEV), u.to(DEV), 1.0, 3).cpu()[:, 0]
     assert set(got.tolist()) == {5, 700, 701}
