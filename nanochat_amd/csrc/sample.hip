@@ -266,13 +266,14 @@ __device__ void row_sample_topk(const SampleParams& p, const float* row, float u
       if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
     });
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int above = 0, b = 255;
-      for (; b > 0; --b) {
-        if (above + static_cast<int>(hist[b]) >= remaining) break;
-        above += hist[b];
-      }
-      misc[0] = b;
+    // the bin holding the remaining-th largest key: thread t < 256 takes bin 255 - t; an
+    // exclusive scan in that order gives the count of keys in higher bins
+    const int bin = 255 - static_cast<int>(threadIdx.x);
+    const int cnt = threadIdx.x < 256 ? static_cast<int>(hist[bin]) : 0;
+    int all;
+    const int above = block_exclusive_scan<int>(cnt, reinterpret_cast<int*>(scan_tmp), all);
+    if (cnt > 0 && above < remaining && remaining <= above + cnt) {
+      misc[0] = bin;
       misc[1] = remaining - above;
     }
     __syncthreads();

@@ -97,6 +97,21 @@ def test_logits_head_equals_torch_softcap_on_same_logits():
     assert torch.equal(got, want)
 
 
+@pytest.mark.parametrize("m,vocab,pad,k,dtype", [(16, 50257, 50304, 768, torch.bfloat16),
+                                                 (64, 32768, 32768, 1536, torch.bfloat16),
+                                                 (8, 5000, 5056, 512, torch.float16)])
+def test_logits_head_vocab_slices_and_dtypes(m, vocab, pad, k, dtype):
+    g = gen(m + vocab)
+    x = randn((m, k), g, dtype).to(DEV)
+    w = (randn((pad, k), g) * 0.3).to(dtype).to(DEV)
+    got = logits_head(x, w, vocab, 15.0)
+    assert got.shape == (m, vocab) and got.dtype == torch.float32
+    want = 15 * torch.tanh(linear(x, w[:vocab]).float() / 15)
+    assert torch.equal(got, want)
+    ref = 15 * torch.tanh((x.double().cpu() @ w[:vocab].double().cpu().T) / 15)
+    assert max_rel_err(got, ref) <= 1e-2
+
+
 def test_logits_head_epilogue_every_bf16_value():
     # x = [1, 0...], W[n, 0] = the n-th bf16 bit pattern: logits are exactly every bf16 value
     vals = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
