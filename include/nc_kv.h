@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define NC_KV_ABI_VERSION 6
+#define NC_KV_ABI_VERSION 7
 
 /* Element types (the torch dtypes the reference path uses). */
 enum nc_dtype {
@@ -73,7 +73,19 @@ enum nc_status {
  * row b reads and appends cache row cache_batch_idx[b] instead of row b;
  * cache_seqlens stays indexed by b.  cache_batch is the number of cache rows.
  * With k/v given the indices must be distinct (rows sharing a cache row race,
- * as in FA3). */
+ * as in FA3).
+ *
+ * page_table (optional, FA3's paged KV cache; not together with
+ * cache_batch_idx): k_cache / v_cache are (num_blocks, page_size, H_kv, D)
+ * blocks, and logical position j of batch row b is slot j % page_size of
+ * block page_table[b * page_table_stride + j / page_size].  t_max is the
+ * logical capacity of a row (at most page_table_stride * page_size);
+ * kc_stride_b / vc_stride_b are the block strides and must equal page_size
+ * times kc_stride_t / vc_stride_t.  page_size is a power of two, at least 16.
+ * A table entry outside [0, num_blocks) is never dereferenced: that key is
+ * not read or stored, the row's output is undefined, and NC_DEVERR_PAGE is
+ * set. */
+#define NC_DEVERR_PAGE 32
 
 /* ---------------------------------------------------------------------------
  * Ragged KV append: k_cache[b, cache_seqlens[b] + t] = k[b, t] (and v), t < t_new.
@@ -93,6 +105,8 @@ typedef struct nc_append_args {
   int64_t cache_batch;           /* cache rows (with cache_batch_idx) */
   const int32_t* cu_seqlens_q;   /* (B+1,) or NULL: packed new tokens */
   int64_t total_q;               /* tokens in k, v (with cu_seqlens_q) */
+  const int32_t* page_table;     /* (B, page_table_stride) or NULL: paged cache */
+  int64_t page_table_stride, page_size, num_blocks;
   int64_t batch, t_new, t_max, n_kv_heads, head_dim;
   int64_t kc_stride_b, kc_stride_t, kc_stride_h;
   int64_t vc_stride_b, vc_stride_t, vc_stride_h;
@@ -162,6 +176,8 @@ typedef struct nc_attn_args {
   int64_t cache_batch;           /* cache rows (with cache_batch_idx) */
   const int32_t* cu_seqlens_q;   /* (B+1,) or NULL: packed query tokens */
   int64_t total_q;               /* tokens in q, k, v, out (with cu_seqlens_q) */
+  const int32_t* page_table;     /* (B, page_table_stride) or NULL: paged cache */
+  int64_t page_table_stride, page_size, num_blocks;
   void* workspace;
   size_t workspace_bytes;
   int64_t batch, t_new, t_max, n_heads, n_kv_heads, head_dim;

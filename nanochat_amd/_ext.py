@@ -16,7 +16,7 @@ import torch
 # NANOCHAT_AMD_LIB points at another build of the same library (e.g. a tuning
 # variant); by default the in-tree build next to this file is loaded.
 LIB_PATH = Path(os.environ.get("NANOCHAT_AMD_LIB", Path(__file__).resolve().parent / "libnc_kv.so"))
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -25,6 +25,7 @@ NC_DEVERR_ROPE_RANGE = 2
 NC_DEVERR_BATCH_IDX = 4
 NC_DEVERR_QLEN = 8
 NC_DEVERR_SAMPLE = 16
+NC_DEVERR_PAGE = 32
 # leading workspace bytes holding split counters: zero before first use, left zero by every call
 NC_WORKSPACE_SYNC_BYTES = 65536
 
@@ -39,6 +40,7 @@ class AppendArgs(ctypes.Structure):
         ("k", _c_void_p), ("v", _c_void_p),
         ("cache_seqlens", _c_void_p), ("error_flag", _c_void_p),
         ("cache_batch_idx", _c_void_p), ("cache_batch", _i64), ("cu_seqlens_q", _c_void_p), ("total_q", _i64),
+        ("page_table", _c_void_p), ("page_table_stride", _i64), ("page_size", _i64), ("num_blocks", _i64),
         ("batch", _i64), ("t_new", _i64), ("t_max", _i64), ("n_kv_heads", _i64), ("head_dim", _i64),
         ("kc_stride_b", _i64), ("kc_stride_t", _i64), ("kc_stride_h", _i64),
         ("vc_stride_b", _i64), ("vc_stride_t", _i64), ("vc_stride_h", _i64),
@@ -66,6 +68,7 @@ class AttnArgs(ctypes.Structure):
         ("k", _c_void_p), ("v", _c_void_p),
         ("cache_seqlens", _c_void_p), ("error_flag", _c_void_p),
         ("cache_batch_idx", _c_void_p), ("cache_batch", _i64), ("cu_seqlens_q", _c_void_p), ("total_q", _i64),
+        ("page_table", _c_void_p), ("page_table_stride", _i64), ("page_size", _i64), ("num_blocks", _i64),
         ("workspace", _c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("batch", _i64), ("t_new", _i64), ("t_max", _i64),
         ("n_heads", _i64), ("n_kv_heads", _i64), ("head_dim", _i64),

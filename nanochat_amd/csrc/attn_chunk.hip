@@ -75,7 +75,8 @@ struct ChunkParams {
   int64_t cache_batch;
   const int32_t* cu_q;       // cu_seqlens_q (packed query tokens) or NULL
   int64_t total_q;
-  int32_t indirect;          // cache_idx or cu_q given: per-row lookups (else row b, t_new queries)
+  PageMap pages;             // paged cache (page_table), or pages.table == NULL
+  int32_t indirect;          // cache_idx, cu_q or a page table given: per-row lookups (else row b, t_new queries)
   int32_t q_bound, len_lo, len_hi;  // varlen rows: validity bound, and the token counts this launch takes
   int64_t q_sb, q_st, q_sh;
   int64_t kc_sb, kc_st, kc_sh;
@@ -181,8 +182,12 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   RowQ rq{b * p.t_new, p.t_new};
   if constexpr (IND) {
     const bool report = qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0;
-    cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
-    if (cb < 0) return;
+    if (p.pages.table == nullptr) {
+      cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
+      if (cb < 0) return;
+    } else {
+      cb = 0;  // paged: every position is addressed through the page table
+    }
     rq = row_queries(p.cu_q, p.total_q, b, p.q_bound, p.err, report);
     if (rq.len < p.len_lo || rq.len > p.len_hi) return;  // another launch's row (or skipped)
   }
@@ -259,9 +264,18 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     koff[u] = static_cast<uint32_t>((key0 + u * KSTEP) * kst + dc0 * 16);
     voff[u] = static_cast<uint32_t>((key0 + u * KSTEP) * vst + dc0 * 16);
   }
+  // physical cache position of logical key j: j, or its page-table slot (-1: not addressable)
+  auto cache_pos = [&](int j) -> int64_t {
+    if constexpr (IND) {
+      if (p.pages.table != nullptr) return page_pos(p.pages, b, j, p.err);
+    }
+    return j;
+  };
+  bool contiguous = true;  // positions are cache rows (no page table)
+  if constexpr (IND) contiguous = p.pages.table == nullptr;
   uint4 kreg[PER_THREAD], vreg[PER_THREAD];
   auto load_regs = [&](int kt0, uint4 (&kr)[PER_THREAD], uint4 (&vr)[PER_THREAD]) {
-    if (kt0 + kBN <= hi && kt0 + kBN <= new_lo) {
+    if (contiguous && kt0 + kBN <= hi && kt0 + kBN <= new_lo) {
       // whole tile inside the span and in the cache: no per-chunk checks
       const char* kt = kbase + kt0 * kst;
       const char* vt = vbase + kt0 * vst;
@@ -275,10 +289,11 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
 #pragma unroll
     for (int u = 0; u < PER_THREAD; ++u) {
       const int j = kt0 + key0 + u * KSTEP;
-      if (j < hi) {
-        const bool from_new = j >= new_lo;
-        const char* kp = from_new ? knew + (j - s) * knst : kbase + j * kst;
-        const char* vp = from_new ? vnew + (j - s) * vnst : vbase + j * vst;
+      const bool from_new = j >= new_lo;
+      const int64_t pj = (j < hi && !from_new) ? cache_pos(j) : 0;
+      if (j < hi && pj >= 0) {
+        const char* kp = from_new ? knew + (j - s) * knst : kbase + pj * kst;
+        const char* vp = from_new ? vnew + (j - s) * vnst : vbase + pj * vst;
         kr[u] = *reinterpret_cast<const uint4*>(kp + dc0 * 16);
         vr[u] = *reinterpret_cast<const uint4*>(vp + dc0 * 16);
       } else {
@@ -304,9 +319,10 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
         const int j = kt0 + key0 + u * KSTEP;
-        if (j >= own_lo && j < hi) {
-          *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + j * kst + dc0 * 16) = kr[u];
-          *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + j * vst + dc0 * 16) = vr[u];
+        const int64_t pj = (j >= own_lo && j < hi) ? cache_pos(j) : -1;
+        if (pj >= 0) {
+          *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + pj * kst + dc0 * 16) = kr[u];
+          *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + pj * vst + dc0 * 16) = vr[u];
         }
       }
     }
@@ -454,7 +470,8 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.seqlens = a.cache_seqlens;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
-  p.indirect = (a.cache_batch_idx != nullptr || a.cu_seqlens_q != nullptr) ? 1 : 0;
+  p.pages = page_map(a.page_table, a.page_table_stride, a.page_size, a.num_blocks);
+  p.indirect = (a.cache_batch_idx != nullptr || a.cu_seqlens_q != nullptr || a.page_table != nullptr) ? 1 : 0;
   p.q_bound = p.len_hi = static_cast<int32_t>(a.t_new);
   p.len_lo = 0;
   if (rows != nullptr) {

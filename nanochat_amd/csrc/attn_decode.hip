@@ -46,7 +46,8 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
-  p.indirect = (a.cache_batch_idx != nullptr || a.cu_seqlens_q != nullptr) ? 1 : 0;
+  p.pages = page_map(a.page_table, a.page_table_stride, a.page_size, a.num_blocks);
+  p.indirect = (a.cache_batch_idx != nullptr || a.cu_seqlens_q != nullptr || a.page_table != nullptr) ? 1 : 0;
   p.q_bound = p.len_hi = static_cast<int32_t>(a.t_new);
   p.len_lo = 0;
   p.part_ml = s.part_ml; p.part_o = s.part_o;

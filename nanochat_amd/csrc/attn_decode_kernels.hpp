@@ -90,7 +90,8 @@ struct DecodeParams {
   int64_t cache_batch;
   const int32_t* cu_q;       // cu_seqlens_q (packed query tokens) or NULL
   int64_t total_q;
-  int32_t indirect;          // cache_idx or cu_q given: per-row lookups (else row b, t_new queries)
+  PageMap pages;             // paged cache (page_table), or pages.table == NULL
+  int32_t indirect;          // cache_idx, cu_q or a page table given: per-row lookups (else row b, t_new queries)
   int32_t q_bound, len_lo, len_hi;  // varlen rows: validity bound, and the token counts this launch takes
   float* part_ml;
   float* part_o;
@@ -426,8 +427,12 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   RowQ rq{b * p.t_new, p.t_new};
   if constexpr (IND) {
     const bool report = split == 0 && t == 0 && hk == 0 && hb == 0 && threadIdx.x == 0;
-    cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
-    if (cb < 0) return;
+    if (p.pages.table == nullptr) {
+      cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
+      if (cb < 0) return;
+    } else {
+      cb = 0;  // paged: every position is addressed through the page table
+    }
     rq = row_queries(p.cu_q, p.total_q, b, p.q_bound, p.err, report);
     // no such query in this row, the row is another launch's, or it was skipped
     if (rq.len < p.len_lo || rq.len > p.len_hi || t >= rq.len) return;
@@ -480,8 +485,17 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     for (int i = 0; i < NI; ++i) {
       const int j = base + i * KPI + row;
       if (j < kc_end) {
-        kv[i] = load16(kbase + j * kst);
-        vv[i] = load16(vbase + j * vst);
+        int64_t pj = j;
+        if constexpr (IND) {
+          if (p.pages.table != nullptr) pj = page_pos(p.pages, b, j, p.err);
+        }
+        if (pj >= 0) {
+          kv[i] = load16(kbase + pj * kst);
+          vv[i] = load16(vbase + pj * vst);
+        } else {
+          kv[i] = make_uint4(0, 0, 0, 0);
+          vv[i] = make_uint4(0, 0, 0, 0);
+        }
       } else {
         kv[i] = make_uint4(0, 0, 0, 0);
         vv[i] = make_uint4(0, 0, 0, 0);
@@ -617,8 +631,14 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     }
     const uint4 vn = load_as_cache_vec<TC>(p.v_new, voff, p.q_dtype);
     if (hb == 0 && row == 0) {
-      *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + qpos * kst) = kn;
-      *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + qpos * vst) = vn;
+      int64_t pq = qpos;
+      if constexpr (IND) {
+        if (p.pages.table != nullptr) pq = page_pos(p.pages, b, qpos, p.err);
+      }
+      if (pq >= 0) {
+        *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + pq * kst) = kn;
+        *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + pq * vst) = vn;
+      }
     }
     float vf[VEC];
     widen<TC>::run(vn, vf);

@@ -23,6 +23,7 @@ struct AppendParams {
   int64_t cache_batch;
   const int32_t* cu_q;       // cu_seqlens_q (packed new tokens) or NULL
   int64_t total_q;
+  PageMap pages;             // paged cache (page_table), or pages.table == NULL
   int64_t kc_sb, kc_st, kc_sh, vc_sb, vc_st, vc_sh;
   int64_t k_sb, k_st, k_sh, v_sb, v_st, v_sh;
   int32_t t_new, t_max, h_kv, vecs_per_head;  // vecs_per_head = D / VEC
@@ -42,15 +43,19 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const AppendParams p) {
   const int h = static_cast<int>(r % p.h_kv); r /= p.h_kv;
   const int t = static_cast<int>(r % p.t_new);
   const int64_t b = r / p.t_new;
-  const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, c == 0 && h == 0 && t == 0 && !is_v);
+  const int64_t cb = p.pages.table != nullptr
+      ? 0 : cache_row(p.cache_idx, p.cache_batch, b, p.err, c == 0 && h == 0 && t == 0 && !is_v);
   if (cb < 0) return;
   const RowQ rq = row_queries(p.cu_q, p.total_q, b, p.t_new, p.err, c == 0 && h == 0 && t == 0 && !is_v);
   if (t >= rq.len) return;
-  const int pos = p.seqlens[b] + t;
-  if (pos < 0 || pos >= p.t_max) {
+  const int lpos = p.seqlens[b] + t;
+  if (lpos < 0 || lpos >= p.t_max) {
     if (p.err != nullptr && c == 0 && h == 0 && !is_v) atomicOr(p.err, NC_DEVERR_OVERFLOW);
     return;
   }
+  // cache row of the position: the page table's slot for paged caches
+  const int64_t pos = p.pages.table != nullptr ? page_pos(p.pages, b, lpos, c == 0 ? p.err : nullptr) : lpos;
+  if (pos < 0) return;
   const void* src = is_v ? p.v : p.k;
   const int64_t soff = is_v ? token_offset(p.cu_q, rq, b, t, p.v_sb, p.v_st) + h * p.v_sh
                             : token_offset(p.cu_q, rq, b, t, p.k_sb, p.k_st) + h * p.k_sh;
@@ -136,6 +141,7 @@ struct RopeAppendParams {
   int64_t cache_batch;
   const int32_t* cu_q;       // cu_seqlens_q (packed tokens) or NULL
   int64_t total_q;
+  PageMap pages;             // paged cache (page_table), or pages.table == NULL
   const void* cos;
   const void* sin;
   int64_t q_sb, q_st, q_sh, k_sb, k_st, k_sh, v_sb, v_st, v_sh;
@@ -200,18 +206,22 @@ __global__ __launch_bounds__(256) void qk_rope_append_kernel(const RopeAppendPar
     for (int e = 0; e < VE; ++e) store_any(p.q_out, o0 + e, p.q_dtype, x[e]);
     return;
   }
-  const int64_t cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, c == 0 && h == 0 && t == 0 && kind == 1);
+  const int64_t cb = p.pages.table != nullptr
+      ? 0 : cache_row(p.cache_idx, p.cache_batch, b, p.err, c == 0 && h == 0 && t == 0 && kind == 1);
   if (cb < 0) return;
   if (pos < 0 || pos >= p.t_max) {
     if (c == 0 && h == 0 && kind == 1 && p.err != nullptr) atomicOr(p.err, NC_DEVERR_OVERFLOW);
     return;
   }
+  // cache row of the position: the page table's slot for paged caches
+  const int64_t cpos = p.pages.table != nullptr ? page_pos(p.pages, b, pos, c == 0 ? p.err : nullptr) : pos;
+  if (cpos < 0) return;
   if (kind == 1) {
-    const int64_t d0 = cb * p.kc_sb + static_cast<int64_t>(pos) * p.kc_st + h * p.kc_sh + c * VE;
+    const int64_t d0 = cb * p.kc_sb + cpos * p.kc_st + h * p.kc_sh + c * VE;
 #pragma unroll
     for (int e = 0; e < VE; ++e) store_any(p.kc, d0 + e, p.cache_dtype, x[e]);
   } else {
-    const int64_t d0 = cb * p.vc_sb + static_cast<int64_t>(pos) * p.vc_st + h * p.vc_sh + c * VE;
+    const int64_t d0 = cb * p.vc_sb + cpos * p.vc_st + h * p.vc_sh + c * VE;
 #pragma unroll
     for (int e = 0; e < VE; ++e) copy_elem(p.vc, d0 + e, p.cache_dtype, p.v, soff + c * VE + e, p.q_dtype);
   }
@@ -225,6 +235,7 @@ hipError_t launch_append(const nc_append_args& a, hipStream_t stream) {
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
+  p.pages = page_map(a.page_table, a.page_table_stride, a.page_size, a.num_blocks);
   p.kc_sb = a.kc_stride_b; p.kc_st = a.kc_stride_t; p.kc_sh = a.kc_stride_h;
   p.vc_sb = a.vc_stride_b; p.vc_st = a.vc_stride_t; p.vc_sh = a.vc_stride_h;
   p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
@@ -254,6 +265,7 @@ hipError_t launch_rope_append(const nc_attn_args& a, const nc_qk_prologue& pro, 
   p.seqlens = a.cache_seqlens; p.err = a.error_flag;
   p.cache_idx = a.cache_batch_idx; p.cache_batch = a.cache_batch;
   p.cu_q = a.cu_seqlens_q; p.total_q = a.total_q;
+  p.pages = page_map(a.page_table, a.page_table_stride, a.page_size, a.num_blocks);
   p.cos = pro.cos; p.sin = pro.sin;
   p.q_sb = a.q_stride_b; p.q_st = a.q_stride_t; p.q_sh = a.q_stride_h;
   p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;

@@ -55,6 +55,18 @@ constexpr int64_t kMergeInKernelMaxWG = NC_DECODE_MERGE_IN_KERNEL ? 2048 : 0;
 bool valid_dtype(int d) { return d == NC_DTYPE_F32 || d == NC_DTYPE_F16 || d == NC_DTYPE_BF16; }
 int64_t dtype_bytes(int d) { return d == NC_DTYPE_F32 ? 4 : 2; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// A paged cache (page_table given): a power-of-two page of at least 16 tokens,
+// blocks of page_size token rows, a table wide enough for t_max positions, and
+// no cache_batch_idx beside it.
+bool valid_pages(const int32_t* table, int64_t stride, int64_t page_size, int64_t num_blocks, int64_t t_max,
+                 const int32_t* cache_batch_idx, int64_t kc_sb, int64_t kc_st, int64_t vc_sb, int64_t vc_st) {
+  if (table == nullptr) return true;
+  if (cache_batch_idx != nullptr) return false;
+  if (page_size < 16 || page_size > (int64_t(1) << 24) || (page_size & (page_size - 1)) != 0) return false;
+  if (num_blocks <= 0 || num_blocks > INT32_MAX || stride < (t_max + page_size - 1) / page_size) return false;
+  return kc_sb == page_size * kc_st && vc_sb == page_size * vc_st;
+}
 bool strides16(int64_t ebytes, int64_t s0, int64_t s1, int64_t s2) {
   return (s0 * ebytes) % 16 == 0 && (s1 * ebytes) % 16 == 0 && (s2 * ebytes) % 16 == 0;
 }
@@ -74,6 +86,10 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   if (a.keys_per_split < 0 || a.keys_per_split % 64 != 0) return NC_ERR_BAD_SHAPE;
   if (a.cache_batch_idx != nullptr && a.cache_batch <= 0) return NC_ERR_BAD_SHAPE;
   if (a.cu_seqlens_q != nullptr && (a.total_q < 0 || a.total_q > INT32_MAX)) return NC_ERR_BAD_SHAPE;
+  if (!valid_pages(a.page_table, a.page_table_stride, a.page_size, a.num_blocks, a.t_max, a.cache_batch_idx,
+                   a.kc_stride_b, a.kc_stride_t, a.vc_stride_b, a.vc_stride_t)) {
+    return NC_ERR_BAD_SHAPE;
+  }
 
   const int group = static_cast<int>(a.n_heads / a.n_kv_heads);
   int hb = 1;
@@ -214,6 +230,10 @@ int nc_kv_append(const nc_append_args* args, void* stream) {
   }
   if (a.cache_batch_idx != nullptr && a.cache_batch <= 0) return NC_ERR_BAD_SHAPE;
   if (a.cu_seqlens_q != nullptr && (a.total_q < 0 || a.total_q > INT32_MAX)) return NC_ERR_BAD_SHAPE;
+  if (!valid_pages(a.page_table, a.page_table_stride, a.page_size, a.num_blocks, a.t_max, a.cache_batch_idx,
+                   a.kc_stride_b, a.kc_stride_t, a.vc_stride_b, a.vc_stride_t)) {
+    return NC_ERR_BAD_SHAPE;
+  }
   if (!valid_dtype(a.in_dtype) || !valid_dtype(a.cache_dtype)) return NC_ERR_DTYPE;
   const int64_t eb = dtype_bytes(a.cache_dtype);
   if ((a.head_dim * eb) % 16 != 0) return NC_ERR_HEAD_DIM;
@@ -308,6 +328,8 @@ int run_attention(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch
       ap.cache_seqlens = a.cache_seqlens; ap.error_flag = a.error_flag;
       ap.cache_batch_idx = a.cache_batch_idx; ap.cache_batch = a.cache_batch;
       ap.cu_seqlens_q = a.cu_seqlens_q; ap.total_q = a.total_q;
+      ap.page_table = a.page_table; ap.page_table_stride = a.page_table_stride;
+      ap.page_size = a.page_size; ap.num_blocks = a.num_blocks;
       ap.batch = a.batch; ap.t_new = a.t_new; ap.t_max = a.t_max;
       ap.n_kv_heads = a.n_kv_heads; ap.head_dim = a.head_dim;
       ap.kc_stride_b = a.kc_stride_b; ap.kc_stride_t = a.kc_stride_t; ap.kc_stride_h = a.kc_stride_h;

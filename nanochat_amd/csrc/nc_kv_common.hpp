@@ -327,6 +327,26 @@ __device__ __forceinline__ int64_t cache_row(const int32_t* idx, int64_t n_rows,
 // queries starting at token b * t_new.  A range that is not inside
 // [0, total_q) or longer than t_new (the launch's bound, max_seqlen_q) gives
 // len = -1: the row is skipped and `report` sets NC_DEVERR_QLEN.
+// Paged cache (page_table): logical position j of batch row b is slot
+// j & (2^shift - 1) of block table[b * stride + (j >> shift)]; the returned
+// physical position indexes the cache as block * 2^shift + slot token rows
+// (the block stride is 2^shift rows).  A block outside [0, n_blocks) returns
+// -1 and sets NC_DEVERR_PAGE: the caller neither reads nor stores that key.
+struct PageMap {
+  const int32_t* table;   // NULL: the cache is not paged
+  int64_t stride;
+  int32_t shift;
+  int64_t n_blocks;
+};
+__device__ __forceinline__ int64_t page_pos(const PageMap& pm, int64_t b, int j, int32_t* err) {
+  const int32_t blk = pm.table[b * pm.stride + (j >> pm.shift)];
+  if (blk < 0 || blk >= pm.n_blocks) {
+    if (err != nullptr) atomicOr(err, NC_DEVERR_PAGE);
+    return -1;
+  }
+  return (static_cast<int64_t>(blk) << pm.shift) | (j & ((1 << pm.shift) - 1));
+}
+
 struct RowQ {
   int64_t tok0;  // token index of the row's first query (row of `out`)
   int len;       // queries of the row

@@ -8,8 +8,16 @@
 #include <algorithm>
 
 #include "nc_kv.h"
+#include "nc_kv_common.hpp"
 
 namespace nckv {
+
+// The device-side page map of a call (table NULL when the cache is not paged).
+inline PageMap page_map(const int32_t* table, int64_t stride, int64_t page_size, int64_t n_blocks) {
+  PageMap pm{table, stride, 0, n_blocks};
+  while (table != nullptr && (int64_t(1) << pm.shift) < page_size) ++pm.shift;
+  return pm;
+}
 
 // Split-K scratch carved out of the caller's workspace.
 struct AttnScratch {

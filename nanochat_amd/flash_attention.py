@@ -68,7 +68,7 @@ def _dtype_code(t: torch.Tensor, name: str) -> int:
 
 
 def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_size, keys_per_split,
-               cache_batch_idx=None, cu_seqlens_q=None, max_seqlen_q=None):
+               cache_batch_idx=None, cu_seqlens_q=None, max_seqlen_q=None, page_table=None):
     """Validate the arguments of one attention call and fill nc_attn_args (workspace left empty).
 
     With cu_seqlens_q, q/k/v are packed tokens (total_q, H or H_kv, D) and the
@@ -100,7 +100,21 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
     Bc, T_max, H_kv, Dc = k_cache.shape
     if tuple(v_cache.shape) != (Bc, T_max, H_kv, Dc):
         raise ValueError(f"v_cache shape {tuple(v_cache.shape)} != k_cache shape {tuple(k_cache.shape)}")
-    if (cache_batch_idx is None and Bc != B) or Dc != D:
+    paged = page_table is not None
+    if paged:
+        # FA3's paged cache: (num_blocks, page_size, H_kv, D) blocks, row b's logical positions
+        # through page_table[b] (B, max_blocks_per_seq) int32
+        if cache_batch_idx is not None:
+            raise ValueError(f"{name}: page_table and cache_batch_idx cannot be combined")
+        if page_table.dim() != 2 or page_table.shape[0] != B or page_table.dtype != torch.int32:
+            raise ValueError(f"{name}: page_table must be a (B, max_blocks) int32 tensor")
+        if page_table.stride(-1) != 1:
+            page_table = page_table.contiguous()
+        page_size, num_blocks = T_max, Bc
+        if page_size < 16 or page_size & (page_size - 1):
+            raise ValueError(f"{name}: the page size (k_cache.shape[1] = {page_size}) must be a power of two >= 16")
+        T_max = page_table.shape[1] * page_size   # logical positions of a row
+    if (cache_batch_idx is None and not paged and Bc != B) or Dc != D:
         raise ValueError(f"cache shape {tuple(k_cache.shape)} does not match q shape {tuple(q.shape)}")
     if cache_batch_idx is not None:
         if tuple(cache_batch_idx.shape) != (B,) or cache_batch_idx.dtype != torch.int32:
@@ -121,6 +135,7 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
     tensors = [q, k_cache, v_cache, cache_seqlens] + ([k, v] if k is not None else [])
     tensors += [cache_batch_idx] if cache_batch_idx is not None else []
     tensors += [cu_seqlens_q] if varlen else []
+    tensors += [page_table] if paged else []
     dev = _require_gpu(name, *tensors)
     for tname, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("k", k), ("v", v)):
         if t is not None and t.stride(-1) != 1:
@@ -141,6 +156,9 @@ def _attn_call(name, q, k_cache, v_cache, k, v, cache_seqlens, causal, window_si
         a.cache_batch_idx, a.cache_batch = cache_batch_idx.data_ptr(), Bc
     if varlen:
         a.cu_seqlens_q, a.total_q = cu_seqlens_q.data_ptr(), total_q
+    if paged:
+        a.page_table, a.page_table_stride = page_table.data_ptr(), page_table.stride(0)
+        a.page_size, a.num_blocks = page_size, num_blocks
     a.batch, a.t_new, a.t_max = B, T_new, T_max
     a.n_heads, a.n_kv_heads, a.head_dim = H, H_kv, D
     if varlen:  # packed tokens: token stride and head stride (the batch stride is unused)
@@ -182,11 +200,13 @@ def _check_device_errors(name, dev):
             raise RuntimeError(f"{name}: cache_batch_idx holds an index outside the cache's batch dimension")
         if bits & _ext.NC_DEVERR_QLEN:
             raise RuntimeError(f"{name}: cu_seqlens_q holds a row outside [0, total_q) or longer than max_seqlen_q")
+        if bits & _ext.NC_DEVERR_PAGE:
+            raise RuntimeError(f"{name}: page_table holds a block index outside the cache")
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
                             causal=False, window_size=(-1, -1), *, cache_batch_idx=None, cu_seqlens_q=None,
-                            max_seqlen_q=None, keys_per_split: int = 0):
+                            max_seqlen_q=None, page_table=None, keys_per_split: int = 0):
     """Append k/v into the cache in place, then attend (see the module docstring).
 
     q: (B, T_new, H, D); k_cache, v_cache: (B, T_max, H_kv, D), or (B_cache, T_max,
@@ -196,10 +216,14 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     cu_seqlens_q: (B+1,) int32 with max_seqlen_q (FA3's varlen layout): q, k, v
     are packed tokens (total_q, H or H_kv, D), row b owning tokens
     [cu[b], cu[b+1]); rows may hold 0, 1 or many tokens.
+    page_table: (B, max_blocks) int32 (FA3's paged cache): k_cache, v_cache are
+    (num_blocks, page_size, H_kv, D) blocks and position j of row b is slot
+    j % page_size of block page_table[b, j // page_size]; page_size a power of two >= 16.
     Returns (B, T_new, H, D), or (total_q, H, D) with cu_seqlens_q, in q's dtype.
     """
     a, out, dev, _ = _attn_call("flash_attn_with_kvcache", q, k_cache, v_cache, k, v, cache_seqlens, causal,
-                                window_size, keys_per_split, cache_batch_idx, cu_seqlens_q, max_seqlen_q)
+                                window_size, keys_per_split, cache_batch_idx, cu_seqlens_q, max_seqlen_q,
+                                page_table)
     L = _ext.lib()
     ref = ctypes.byref(a)
     stream = _ext.stream_handle(dev)
@@ -211,7 +235,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
 
 def flash_attn_with_kvcache_rope(q, k_cache, v_cache, k, v, cache_seqlens, cos, sin, causal=True,
                                  window_size=(-1, -1), *, qk_scale: float = 1.2, eps=None,
-                                 cache_batch_idx=None, cu_seqlens_q=None, max_seqlen_q=None,
+                                 cache_batch_idx=None, cu_seqlens_q=None, max_seqlen_q=None, page_table=None,
                                  keys_per_split: int = 0):
     """flash_attn_with_kvcache with nanochat's QK prologue fused (nanochat/gpt.py:98-102).
 
@@ -239,7 +263,8 @@ def flash_attn_with_kvcache_rope(q, k_cache, v_cache, k, v, cache_seqlens, cos, 
     if not sin2.is_contiguous() or sin2.data_ptr() % 16 != 0:
         sin2 = sin2.clone(memory_format=torch.contiguous_format)
     a, out, dev, _ = _attn_call("flash_attn_with_kvcache_rope", q, k_cache, v_cache, k, v, cache_seqlens, causal,
-                                window_size, keys_per_split, cache_batch_idx, cu_seqlens_q, max_seqlen_q)
+                                window_size, keys_per_split, cache_batch_idx, cu_seqlens_q, max_seqlen_q,
+                                page_table)
     _require_gpu("flash_attn_with_kvcache_rope", cos2, sin2)
     pro = _ext.QKPrologue()
     pro.cos, pro.sin = cos2.data_ptr(), sin2.data_ptr()

@@ -27,6 +27,13 @@ It restates, with the same torch operations the reference uses:
                                stays indexed by b.  Pinned by the permutation
                                identity in tests/test_oracle.py (no golden vectors:
                                the reference never passes it).
+  - page_table                 FA3's paged KV cache through the same branch: caches
+                               are (num_blocks, P, H_kv, D) blocks, position j of row b
+                               is slot j % P of block page_table[b, j // P]; restated as
+                               the call on the rows the table assembles (gather), written
+                               back block by block.  Pinned by the block-shuffle identity
+                               in tests/test_oracle.py (a dense cache cut into blocks and
+                               stored in a shuffled pool gives the dense call's results).
   - cu_seqlens_q               FA3's varlen layout through the same branch: packed
                                tokens, row b owning [cu[b], cu[b+1]); restated as one
                                call per row of the function above, pinned by the
@@ -89,9 +96,25 @@ def kv_append(k_cache, v_cache, k, v, cache_seqlens):
         v_cache[b, pos:pos + T_new, :, :] = v[b]
 
 
+def paged_to_dense(cache_blocks, page_table):
+    """(num_blocks, P, H, D) blocks and a (B, nb) table -> (B, nb * P, H, D) row caches (a copy)."""
+    B, nb = page_table.shape
+    P = cache_blocks.shape[1]
+    return cache_blocks[page_table.long()].reshape(B, nb * P, *cache_blocks.shape[2:])
+
+
+def dense_to_paged(dense, cache_blocks, page_table):
+    """Write (B, nb * P, H, D) row caches back into the blocks their table names."""
+    B, nb = page_table.shape
+    P = cache_blocks.shape[1]
+    for b in range(B):
+        for j in range(nb):
+            cache_blocks[int(page_table[b, j])] = dense[b, j * P:(j + 1) * P]
+
+
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
                             causal=False, window_size=(-1, -1), compute_dtype=None, cache_batch_idx=None,
-                            cu_seqlens_q=None):
+                            cu_seqlens_q=None, page_table=None):
     """nanochat/flash_attention.py:155-177, one batch row at a time.
 
     Mutates k_cache/v_cache like the reference.  ``compute_dtype`` (default:
@@ -99,8 +122,19 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=N
     the result is returned in q's dtype.  ``cache_batch_idx`` (FA3): row b
     uses cache row cache_batch_idx[b].  ``cu_seqlens_q`` (FA3 varlen): q, k, v
     are packed tokens (total_q, H, D) and row b owns [cu[b], cu[b+1]); the
-    output is packed the same way.
+    output is packed the same way.  ``page_table`` (FA3's paged cache): the
+    caches are (num_blocks, P, H, D) blocks and position j of row b is slot
+    j % P of block page_table[b, j // P]; restated as the call on the rows the
+    table assembles, written back block by block.
     """
+    if page_table is not None:
+        kd, vd = paged_to_dense(k_cache, page_table), paged_to_dense(v_cache, page_table)
+        y = flash_attn_with_kvcache(q, kd, vd, k=k, v=v, cache_seqlens=cache_seqlens, causal=causal,
+                                    window_size=window_size, compute_dtype=compute_dtype,
+                                    cu_seqlens_q=cu_seqlens_q)
+        dense_to_paged(kd, k_cache, page_table)
+        dense_to_paged(vd, v_cache, page_table)
+        return y
     if cu_seqlens_q is not None:
         outs = []
         for b in range(len(cu_seqlens_q) - 1):

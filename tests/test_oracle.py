@@ -382,3 +382,32 @@ def test_qk_prologue_detects_planted_sign_mistake(monkeypatch):
     monkeypatch.setattr(orc, "rotary", wrong)
     out = orc.rotary(x, cos_t[idx][:, :, None, :], sin_t[idx][:, :, None, :])
     assert not torch.allclose(out, ref, atol=1e-6)
+
+
+@pytest.mark.parametrize("T_new,with_kv,P", [(1, True, 16), (5, True, 32), (3, False, 16)])
+def test_paged_cache_is_a_block_shuffle_of_the_dense_cache(T_new, with_kv, P):
+    """A dense (B, T, H_kv, D) cache cut into P-token blocks and stored in a shuffled pool (with
+    spare blocks) gives the dense call's outputs, and the pool read back through the table
+    equals the dense cache after the call (append included)."""
+    g = gen(50 + T_new + P)
+    B, H, H_kv, D, nb = 3, 4, 2, 16, 4
+    T = nb * P
+    q = randn((B, T_new, H, D), g)
+    kd = randn((B, T, H_kv, D), g)
+    vd = randn((B, T, H_kv, D), g)
+    k = randn((B, T_new, H_kv, D), g) if with_kv else None
+    v = randn((B, T_new, H_kv, D), g) if with_kv else None
+    seqlens = torch.tensor([0, 17, T - T_new], dtype=torch.int32)
+    perm = torch.randperm(B * nb + 5, generator=g)[:B * nb]          # 5 spare blocks never named
+    table = perm.view(B, nb).to(torch.int32)
+    kp = torch.full((B * nb + 5, P, H_kv, D), float("nan"))
+    vp = torch.full((B * nb + 5, P, H_kv, D), float("nan"))
+    orc.dense_to_paged(kd, kp, table)
+    orc.dense_to_paged(vd, vp, table)
+    y_dense = orc.flash_attn_with_kvcache(q, kd, vd, k=k, v=v, cache_seqlens=seqlens, window_size=(-1, 0))
+    y_paged = orc.flash_attn_with_kvcache(q, kp, vp, k=k, v=v, cache_seqlens=seqlens, window_size=(-1, 0),
+                                          page_table=table)
+    assert torch.equal(y_dense, y_paged)
+    assert torch.equal(orc.paged_to_dense(kp, table), kd) and torch.equal(orc.paged_to_dense(vp, table), vd)
+    spare = [i for i in range(B * nb + 5) if i not in set(perm.tolist())]
+    assert torch.isnan(kp[spare]).all()                                # blocks outside the table untouched
