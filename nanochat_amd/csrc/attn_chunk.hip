@@ -133,9 +133,10 @@ template <> struct mfma_t<f16> {
   }
 };
 
-// IND: the launch passes cache_batch_idx or cu_seqlens_q (per-row lookups);
-// plain launches use kernels without the lookup code (3% on the C5 batch).
-template <typename TC, int D, int GB, bool IND>
+// LK: 0 plain launch, with no lookup code (it cost 3% on the C5 batch); 1
+// cache_batch_idx / cu_seqlens_q lookups; 2 those and a page table (kernels of
+// their own, so the lookup kernels keep their code).
+template <typename TC, int D, int GB, int LK>
 __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const ChunkParams p) {
   typedef typename mfma_t<TC>::v8 v8;
   constexpr int QB = kRows / GB;          // queries per workgroup
@@ -180,13 +181,13 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   // invalid entry skips the row in every workgroup of it
   int64_t cb = b;
   RowQ rq{b * p.t_new, p.t_new};
-  if constexpr (IND) {
+  if constexpr (LK != 0) {
     const bool report = qt == 0 && split == 0 && hk == 0 && hb == 0 && tid == 0;
-    if (p.pages.table == nullptr) {
+    if constexpr (LK == 2) {
+      cb = 0;  // paged: every position is addressed through the page table
+    } else {
       cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
       if (cb < 0) return;
-    } else {
-      cb = 0;  // paged: every position is addressed through the page table
     }
     rq = row_queries(p.cu_q, p.total_q, b, p.q_bound, p.err, report);
     if (rq.len < p.len_lo || rq.len > p.len_hi) return;  // another launch's row (or skipped)
@@ -266,13 +267,10 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   }
   // physical cache position of logical key j: j, or its page-table slot (-1: not addressable)
   auto cache_pos = [&](int j) -> int64_t {
-    if constexpr (IND) {
-      if (p.pages.table != nullptr) return page_pos(p.pages, b, j, p.err);
-    }
+    if constexpr (LK == 2) return page_pos(p.pages, b, j, p.err);
     return j;
   };
-  bool contiguous = true;  // positions are cache rows (no page table)
-  if constexpr (IND) contiguous = p.pages.table == nullptr;
+  constexpr bool contiguous = LK != 2;  // positions are cache rows (no page table)
   uint4 kreg[PER_THREAD], vreg[PER_THREAD];
   auto load_regs = [&](int kt0, uint4 (&kr)[PER_THREAD], uint4 (&vr)[PER_THREAD]) {
     if (contiguous && kt0 + kBN <= hi && kt0 + kBN <= new_lo) {
@@ -286,14 +284,31 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
       }
       return;
     }
+    if (!contiguous) {  // paged cache: each cached key's slot from the page table
+#pragma unroll
+      for (int u = 0; u < PER_THREAD; ++u) {
+        const int j = kt0 + key0 + u * KSTEP;
+        const bool from_new = j >= new_lo;
+        const int64_t pj = (j < hi && !from_new) ? cache_pos(j) : 0;
+        if (j < hi && pj >= 0) {
+          const char* kp = from_new ? knew + (j - s) * knst : kbase + pj * kst;
+          const char* vp = from_new ? vnew + (j - s) * vnst : vbase + pj * vst;
+          kr[u] = *reinterpret_cast<const uint4*>(kp + dc0 * 16);
+          vr[u] = *reinterpret_cast<const uint4*>(vp + dc0 * 16);
+        } else {
+          kr[u] = make_uint4(0, 0, 0, 0);
+          vr[u] = make_uint4(0, 0, 0, 0);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int u = 0; u < PER_THREAD; ++u) {
       const int j = kt0 + key0 + u * KSTEP;
-      const bool from_new = j >= new_lo;
-      const int64_t pj = (j < hi && !from_new) ? cache_pos(j) : 0;
-      if (j < hi && pj >= 0) {
-        const char* kp = from_new ? knew + (j - s) * knst : kbase + pj * kst;
-        const char* vp = from_new ? vnew + (j - s) * vnst : vbase + pj * vst;
+      if (j < hi) {
+        const bool from_new = j >= new_lo;
+        const char* kp = from_new ? knew + (j - s) * knst : kbase + j * kst;
+        const char* vp = from_new ? vnew + (j - s) * vnst : vbase + j * vst;
         kr[u] = *reinterpret_cast<const uint4*>(kp + dc0 * 16);
         vr[u] = *reinterpret_cast<const uint4*>(vp + dc0 * 16);
       } else {
@@ -319,7 +334,8 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
         const int j = kt0 + key0 + u * KSTEP;
-        const int64_t pj = (j >= own_lo && j < hi) ? cache_pos(j) : -1;
+        const bool own = j >= own_lo && j < hi;
+        const int64_t pj = own ? (contiguous ? j : cache_pos(j)) : -1;
         if (pj >= 0) {
           *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + pj * kst + dc0 * 16) = kr[u];
           *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + pj * vst + dc0 * 16) = vr[u];
@@ -432,22 +448,23 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   }
 }
 
-template <typename TC, int D, bool IND>
+template <typename TC, int D, int LK>
 hipError_t launch_ci(const ChunkParams& p, int gb, hipStream_t stream) {
   const int64_t n_wg = static_cast<int64_t>(kXcdsC) * p.n_qtiles * p.num_splits * ((p.n_groups + kXcdsC - 1) / kXcdsC);
   const dim3 grid(static_cast<unsigned>(n_wg)), block(kChunkWaves * kWave);
   switch (gb) {
-    case 8: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 8, IND>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 4, IND>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 2, IND>), grid, block, 0, stream, p); break;
-    default: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 1, IND>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 8, LK>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 4, LK>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 2, LK>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 1, LK>), grid, block, 0, stream, p); break;
   }
   return hipGetLastError();
 }
 
 template <typename TC, int D>
 hipError_t launch_c(const ChunkParams& p, int gb, hipStream_t stream) {
-  return p.indirect ? launch_ci<TC, D, true>(p, gb, stream) : launch_ci<TC, D, false>(p, gb, stream);
+  if (p.pages.table != nullptr) return launch_ci<TC, D, 2>(p, gb, stream);
+  return p.indirect ? launch_ci<TC, D, 1>(p, gb, stream) : launch_ci<TC, D, 0>(p, gb, stream);
 }
 
 }  // namespace

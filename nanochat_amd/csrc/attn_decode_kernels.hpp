@@ -380,7 +380,10 @@ __device__ __forceinline__ float coherent_load(const float* p) {
 // gives at most 8 slots per row at 2048 keys)
 constexpr int kInKernelMergeChunk = 8;
 
-template <typename TC, bool QPK, int D, int GB, int NW, bool IND>
+// LK: 0 plain launch (no lookup code); 1 cache_batch_idx / cu_seqlens_q
+// lookups; 2 those and a page table.  Paged launches have kernels of their
+// own so the lookup kernels keep the code they had without paging.
+template <typename TC, bool QPK, int D, int GB, int NW, int LK>
 __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodeParams p) {
   constexpr int VEC = widen<TC>::N;
   constexpr int LPK = D / VEC;            // lanes per key row
@@ -425,13 +428,13 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   // invalid entry skips the row in every workgroup of it
   int64_t cb = b;
   RowQ rq{b * p.t_new, p.t_new};
-  if constexpr (IND) {
+  if constexpr (LK != 0) {
     const bool report = split == 0 && t == 0 && hk == 0 && hb == 0 && threadIdx.x == 0;
-    if (p.pages.table == nullptr) {
+    if constexpr (LK == 2) {
+      cb = 0;  // paged: every position is addressed through the page table
+    } else {
       cb = cache_row(p.cache_idx, p.cache_batch, b, p.err, report);
       if (cb < 0) return;
-    } else {
-      cb = 0;  // paged: every position is addressed through the page table
     }
     rq = row_queries(p.cu_q, p.total_q, b, p.q_bound, p.err, report);
     // no such query in this row, the row is another launch's, or it was skipped
@@ -481,21 +484,22 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
 
   // ---- stream the split's cache keys, TILE keys per wave per step ----
   auto load_tile = [&](int base, uint4 (&kv)[NI], uint4 (&vv)[NI]) {
+    if constexpr (LK == 2) {  // paged cache: each key's slot from the page table
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int j = base + i * KPI + row;
+        const int64_t pj = j < kc_end ? page_pos(p.pages, b, j, p.err) : -1;
+        kv[i] = pj >= 0 ? load16(kbase + pj * kst) : make_uint4(0, 0, 0, 0);
+        vv[i] = pj >= 0 ? load16(vbase + pj * vst) : make_uint4(0, 0, 0, 0);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int j = base + i * KPI + row;
       if (j < kc_end) {
-        int64_t pj = j;
-        if constexpr (IND) {
-          if (p.pages.table != nullptr) pj = page_pos(p.pages, b, j, p.err);
-        }
-        if (pj >= 0) {
-          kv[i] = load16(kbase + pj * kst);
-          vv[i] = load16(vbase + pj * vst);
-        } else {
-          kv[i] = make_uint4(0, 0, 0, 0);
-          vv[i] = make_uint4(0, 0, 0, 0);
-        }
+        kv[i] = load16(kbase + j * kst);
+        vv[i] = load16(vbase + j * vst);
       } else {
         kv[i] = make_uint4(0, 0, 0, 0);
         vv[i] = make_uint4(0, 0, 0, 0);
@@ -632,9 +636,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     const uint4 vn = load_as_cache_vec<TC>(p.v_new, voff, p.q_dtype);
     if (hb == 0 && row == 0) {
       int64_t pq = qpos;
-      if constexpr (IND) {
-        if (p.pages.table != nullptr) pq = page_pos(p.pages, b, qpos, p.err);
-      }
+      if constexpr (LK == 2) pq = page_pos(p.pages, b, qpos, p.err);
       if (pq >= 0) {
         *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + pq * kst) = kn;
         *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + pq * vst) = vn;
@@ -796,27 +798,28 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
 }
 
 
-template <typename TC, bool QPK, int D, int GB, bool IND>
+template <typename TC, bool QPK, int D, int GB, int LK>
 hipError_t launch_gi(const DecodeParams& p, int64_t n_wg, bool wide, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(n_wg));
   if constexpr (GB <= 4 && GB * D <= kWideMaxElems) {
     if (wide) {
-      hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWideWaves, IND>), grid, dim3(kWideWaves * kWave), 0,
+      hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWideWaves, LK>), grid, dim3(kWideWaves * kWave), 0,
                          stream, p);
-      if (p.num_splits > 1 && p.tickets == nullptr) launch_merge_i<D, GB, IND>(p, stream);
+      if (p.num_splits > 1 && p.tickets == nullptr) launch_merge_i<D, GB, (LK != 0)>(p, stream);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWavesPerWG, IND>), grid, dim3(kWavesPerWG * kWave), 0,
+  hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWavesPerWG, LK>), grid, dim3(kWavesPerWG * kWave), 0,
                      stream, p);
-  if (p.num_splits > 1 && p.tickets == nullptr) launch_merge_i<D, GB, IND>(p, stream);
+  if (p.num_splits > 1 && p.tickets == nullptr) launch_merge_i<D, GB, (LK != 0)>(p, stream);
   return hipGetLastError();
 }
 
 template <typename TC, bool QPK, int D, int GB>
 hipError_t launch_g(const DecodeParams& p, int64_t n_wg, bool wide, hipStream_t stream) {
-  return p.indirect ? launch_gi<TC, QPK, D, GB, true>(p, n_wg, wide, stream)
-                    : launch_gi<TC, QPK, D, GB, false>(p, n_wg, wide, stream);
+  if (p.pages.table != nullptr) return launch_gi<TC, QPK, D, GB, 2>(p, n_wg, wide, stream);
+  return p.indirect ? launch_gi<TC, QPK, D, GB, 1>(p, n_wg, wide, stream)
+                    : launch_gi<TC, QPK, D, GB, 0>(p, n_wg, wide, stream);
 }
 
 template <typename TC, bool QPK, int D>
