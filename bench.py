@@ -444,6 +444,56 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
     return out
 
 
+def run_paged(dev, stream, steps, kps=0, ckps=0, page=256):
+    """C2's decode workload (d20, B=32, 20 layers, lengths U[512, 2048] seed 0) through a paged cache
+    (FA3's page_table: `page`-token blocks in a shuffled pool, one table per row) against the same
+    workload on the dense cache, in one process: the cost of addressing keys through the table."""
+    from nanochat_amd.flash_attention import flash_attn_with_kvcache
+    L, B, H, D = LAYERS, BATCH, HEADS, HEAD_DIM
+    seq = c2_seqlens()
+    nb = (T_MAX + page - 1) // page
+    with torch.cuda.stream(stream):
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        kc = torch.randn((L, B, nb * page, KV_HEADS, D), generator=g, device=dev, dtype=torch.bfloat16)
+        vc = torch.randn_like(kc)
+        qs = torch.randn((steps, L, B, 1, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        ks, vs = torch.randn_like(qs[:, :, :, :, :KV_HEADS]), torch.randn_like(qs[:, :, :, :, :KV_HEADS])
+        sl = seq.to(dev)
+        # each layer's pool holds the same blocks as its dense cache, shuffled; row b's table names them
+        perm = torch.randperm(B * nb, generator=torch.Generator().manual_seed(1))
+        table = perm.view(B, nb).to(torch.int32).to(dev)
+        inv = torch.argsort(perm).to(dev)
+        kp = kc.view(L, B * nb, page, KV_HEADS, D)[:, inv].contiguous()
+        vp = vc.view(L, B * nb, page, KV_HEADS, D)[:, inv].contiguous()
+
+    def body(paged):
+        def run():
+            for i in range(steps):
+                for layer in range(L):
+                    if paged:
+                        flash_attn_with_kvcache(qs[i, layer], kp[layer], vp[layer], k=ks[i, layer], v=vs[i, layer],
+                                                cache_seqlens=sl, causal=True, window_size=(-1, 0),
+                                                page_table=table, keys_per_split=kps)
+                    else:
+                        flash_attn_with_kvcache(qs[i, layer], kc[layer], vc[layer], k=ks[i, layer], v=vs[i, layer],
+                                                cache_seqlens=sl, causal=True, window_size=(-1, 0),
+                                                keys_per_split=kps)
+                sl.add_(1)
+        return run
+
+    reset = lambda: sl.copy_(seq.to(dev))  # noqa: E731
+    ms_dense = _graph_time(stream, body(False), reset)
+    ms_paged = _graph_time(stream, body(True), reset)
+    total = sum(step_bytes([int(s) + i for s in seq]) for i in range(steps))
+    gb_d, gb_p = total / (ms_dense * 1e-3) / 1e9, total / (ms_paged * 1e-3) / 1e9
+    return {"config": "paged", "workload": f"C2 decode (d20, B=32, 20 layers) through {page}-token pages of a "
+                                           f"shuffled pool vs the dense cache, {steps} steps",
+            "dense_ms_per_step": round(ms_dense / steps, 5), "paged_ms_per_step": round(ms_paged / steps, 5),
+            "dense_GB_per_s": round(gb_d, 1), "paged_GB_per_s": round(gb_p, 1),
+            "paged_pct_of_peak": round(100 * gb_p / HBM_PEAK_GBPS, 2)}
+
+
 def run_head(dev, stream, steps, kps=0, ckps=0):
     """The decode step's tail on d20 shapes (B=32, 1280 -> 32768 vocab, bf16 weights): the logits head
     (lm_head + slice + fp32 + softcap 15, gpt.py:468-472) as one nc_linear call against F.linear + torch's
@@ -518,9 +568,10 @@ def main() -> int:
     ap.add_argument("--chunk-keys-per-split", type=int, default=0,
                     help="c3/c5 chunk-kernel split size (0 = library default)")
     ap.add_argument("--eager", action="store_true", help="also time the steps without a graph")
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "e2e", "head"],
+    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "e2e", "head", "paged"],
                     help="c2 (default) is the metric line; c3/c4/c5 print per-phase figures; e2e times the d20 "
-                         "model's decode step; head the fused logits head and the sampler")
+                         "model's decode step; head the fused logits head and the sampler; paged C2 through "
+                         "a page table")
     ap.add_argument("--rope", action="store_true",
                     help="c2 through flash_attn_with_kvcache_rope (QK prologue fused; same bytes + tables)")
     args = ap.parse_args()
@@ -535,9 +586,10 @@ def main() -> int:
         dev = torch.device("cuda", 0)
         torch.cuda.set_device(dev)
         stream = torch.cuda.Stream(device=dev)
-        runner = {"c3": run_c3, "c4": run_c4, "c5": run_c5, "e2e": run_e2e, "head": run_head}[args.config]
+        runner = {"c3": run_c3, "c4": run_c4, "c5": run_c5, "e2e": run_e2e, "head": run_head,
+                  "paged": run_paged}[args.config]
         steps = {"c3": min(args.steps, 128), "c4": min(args.steps, 256), "c5": min(args.steps, 16),
-                 "e2e": min(args.steps, 64), "head": min(args.steps, 50)}[args.config]
+                 "e2e": min(args.steps, 64), "head": min(args.steps, 50), "paged": min(args.steps, 200)}[args.config]
         print(json.dumps(runner(dev, stream, steps, kps=args.keys_per_split, ckps=args.chunk_keys_per_split)),
               flush=True)
         return 0

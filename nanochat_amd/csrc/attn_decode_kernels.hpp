@@ -379,6 +379,9 @@ __device__ __forceinline__ float coherent_load(const float* p) {
 // slots folded per round trip by the in-kernel merge (the default split
 // gives at most 8 slots per row at 2048 keys)
 constexpr int kInKernelMergeChunk = 8;
+// Paged cache: a split's page numbers are staged in LDS when it spans at most
+// this many pages (else each key reads the table itself).
+constexpr int kMaxSplitPages = 64;
 
 // LK: 0 plain launch (no lookup code); 1 cache_batch_idx / cu_seqlens_q
 // lookups; 2 those and a page table.  Paged launches have kernels of their
@@ -452,6 +455,38 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   const bool own_new = new_in_range && kr.n > 0 && k1 == qpos + 1;
   const int kc_end = own_new ? k1 - 1 : k1;       // keys read from the cache: [k0, kc_end)
 
+  // paged cache: the page numbers of this split's positions [k0, k1), read
+  // from the table once into LDS (entries outside the pool become -1 and set
+  // NC_DEVERR_PAGE).  Per-key lookups then wait on LDS, not on the vector
+  // memory counter the K/V loads in flight also use.
+  [[maybe_unused]] int page_lo = 0;
+  [[maybe_unused]] bool pages_staged = false;
+  [[maybe_unused]] const int32_t* sm_pg = nullptr;
+  if constexpr (LK == 2) {
+    __shared__ int32_t sm_pages[kMaxSplitPages];
+    page_lo = k0 >> p.pages.shift;
+    const int npages = k1 > k0 ? ((k1 - 1) >> p.pages.shift) - page_lo + 1 : 0;
+    pages_staged = npages <= kMaxSplitPages;
+    if (pages_staged) {
+      for (int i = tid; i < npages; i += NW * kWave) {
+        const int32_t blk = p.pages.table[b * p.pages.stride + page_lo + i];
+        const bool ok = blk >= 0 && blk < p.pages.n_blocks;
+        if (!ok && p.err != nullptr) atomicOr(p.err, NC_DEVERR_PAGE);
+        sm_pages[i] = ok ? blk : -1;
+      }
+      __syncthreads();
+    }
+    sm_pg = sm_pages;
+  }
+  // physical row of cached position j (paged: its page-table slot; -1 if not addressable)
+  auto paged_row = [&](int j) -> int64_t {
+    if (pages_staged) {
+      const int32_t blk = sm_pg[(j >> p.pages.shift) - page_lo];
+      return blk >= 0 ? ((static_cast<int64_t>(blk) << p.pages.shift) | (j & ((1 << p.pages.shift) - 1))) : -1;
+    }
+    return page_pos(p.pages, b, j, p.err);
+  };
+
   if (p.fused && (qpos < 0 || qpos >= p.t_max) && split == 0 && hk == 0 && hb == 0 && tid == 0 &&
       p.err != nullptr) {
     atomicOr(p.err, NC_DEVERR_OVERFLOW);
@@ -488,7 +523,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
         const int j = base + i * KPI + row;
-        const int64_t pj = j < kc_end ? page_pos(p.pages, b, j, p.err) : -1;
+        const int64_t pj = j < kc_end ? paged_row(j) : -1;
         kv[i] = pj >= 0 ? load16(kbase + pj * kst) : make_uint4(0, 0, 0, 0);
         vv[i] = pj >= 0 ? load16(vbase + pj * vst) : make_uint4(0, 0, 0, 0);
       }
@@ -636,7 +671,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     const uint4 vn = load_as_cache_vec<TC>(p.v_new, voff, p.q_dtype);
     if (hb == 0 && row == 0) {
       int64_t pq = qpos;
-      if constexpr (LK == 2) pq = page_pos(p.pages, b, qpos, p.err);
+      if constexpr (LK == 2) pq = paged_row(qpos);
       if (pq >= 0) {
         *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + pq * kst) = kn;
         *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + pq * vst) = vn;
