@@ -487,11 +487,31 @@ def run_paged(dev, stream, steps, kps=0, ckps=0, page=256):
     ms_paged = _graph_time(stream, body(True), reset)
     total = sum(step_bytes([int(s) + i for s in seq]) for i in range(steps))
     gb_d, gb_p = total / (ms_dense * 1e-3) / 1e9, total / (ms_paged * 1e-3) / 1e9
+
+    # chunked prefill: a 128-token chunk per row into the same caches at the C2 lengths (20 layers, MFMA kernel)
+    tc = 128
+    with torch.cuda.stream(stream):
+        qc = torch.randn((L, B, tc, H, D), generator=g, device=dev, dtype=torch.bfloat16)
+        kn, vn = torch.randn_like(qc[:, :, :, :KV_HEADS]), torch.randn_like(qc[:, :, :, :KV_HEADS])
+
+    def chunk_body(paged):
+        def run():
+            for layer in range(L):
+                kcl, vcl = (kp[layer], vp[layer]) if paged else (kc[layer], vc[layer])
+                flash_attn_with_kvcache(qc[layer], kcl, vcl, k=kn[layer], v=vn[layer], cache_seqlens=sl,
+                                        causal=True, window_size=(-1, 0), page_table=table if paged else None,
+                                        keys_per_split=ckps)
+        return run
+
+    ms_chunk_dense = _graph_time(stream, chunk_body(False), reset, reps=steps)
+    ms_chunk_paged = _graph_time(stream, chunk_body(True), reset, reps=steps)
     return {"config": "paged", "workload": f"C2 decode (d20, B=32, 20 layers) through {page}-token pages of a "
-                                           f"shuffled pool vs the dense cache, {steps} steps",
+                                           f"shuffled pool vs the dense cache, {steps} steps; and one "
+                                           f"{tc}-token chunk per row into the same caches, 20 layers",
             "dense_ms_per_step": round(ms_dense / steps, 5), "paged_ms_per_step": round(ms_paged / steps, 5),
             "dense_GB_per_s": round(gb_d, 1), "paged_GB_per_s": round(gb_p, 1),
-            "paged_pct_of_peak": round(100 * gb_p / HBM_PEAK_GBPS, 2)}
+            "paged_pct_of_peak": round(100 * gb_p / HBM_PEAK_GBPS, 2),
+            "chunk_dense_ms": round(ms_chunk_dense, 5), "chunk_paged_ms": round(ms_chunk_paged, 5)}
 
 
 def run_head(dev, stream, steps, kps=0, ckps=0):

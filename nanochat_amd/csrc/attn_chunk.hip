@@ -53,6 +53,7 @@ namespace {
 constexpr int kChunkWaves = 4;
 constexpr int kRows = 64;        // (query, head) rows per workgroup
 constexpr int kBN = 64;          // keys per tile
+constexpr int kChunkStagePages = 512;  // page numbers a workgroup stages in LDS (paged cache)
 constexpr float kNegBigC = -1.0e30f;
 constexpr int kXcdsC = 8;
 
@@ -265,9 +266,41 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     koff[u] = static_cast<uint32_t>((key0 + u * KSTEP) * kst + dc0 * 16);
     voff[u] = static_cast<uint32_t>((key0 + u * KSTEP) * vst + dc0 * 16);
   }
-  // physical cache position of logical key j: j, or its page-table slot (-1: not addressable)
+  // paged cache: the page numbers of this workgroup's keys [lo, hi), read from
+  // the table once into LDS (entries outside the pool become -1 and set
+  // NC_DEVERR_PAGE), so a tile's K/V loads wait on LDS rather than on a table
+  // load of their own.  Spans of more pages fall back to per-key lookups, and
+  // so do workgroups that read no cached key (a prefill from position 0: only
+  // their stores look pages up, and a staging prologue would only add latency).
+  [[maybe_unused]] int page_lo = 0;
+  [[maybe_unused]] bool pages_staged = false;
+  [[maybe_unused]] const int32_t* sm_pg = nullptr;
+  if constexpr (LK == 2) {
+    __shared__ int32_t sm_pages[kChunkStagePages];
+    page_lo = lo >> p.pages.shift;
+    const int npages = hi > lo ? ((hi - 1) >> p.pages.shift) - page_lo + 1 : 0;
+    pages_staged = npages <= kChunkStagePages && min(hi, new_lo) > lo;
+    if (pages_staged) {
+      for (int i = tid; i < npages; i += kChunkWaves * kWave) {
+        const int32_t blk = p.pages.table[b * p.pages.stride + page_lo + i];
+        const bool ok = blk >= 0 && blk < p.pages.n_blocks;
+        if (!ok && p.err != nullptr) atomicOr(p.err, NC_DEVERR_PAGE);
+        sm_pages[i] = ok ? blk : -1;
+      }
+      __syncthreads();
+    }
+    sm_pg = sm_pages;
+  }
+  // physical cache position of logical key j in [lo, hi): j, or its page-table
+  // slot (-1: not addressable)
   auto cache_pos = [&](int j) -> int64_t {
-    if constexpr (LK == 2) return page_pos(p.pages, b, j, p.err);
+    if constexpr (LK == 2) {
+      if (pages_staged) {
+        const int32_t blk = sm_pg[(j >> p.pages.shift) - page_lo];
+        return blk >= 0 ? ((static_cast<int64_t>(blk) << p.pages.shift) | (j & ((1 << p.pages.shift) - 1))) : -1;
+      }
+      return page_pos(p.pages, b, j, p.err);
+    }
     return j;
   };
   constexpr bool contiguous = LK != 2;  // positions are cache rows (no page table)
@@ -285,6 +318,22 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
       return;
     }
     if (!contiguous) {  // paged cache: each cached key's slot from the page table
+      if (pages_staged && kt0 + kBN <= hi && kt0 + kBN <= new_lo) {
+        // whole tile in the cache: branch-free loads (a key of a page outside
+        // the pool reads block 0, which exists, and is then zeroed)
+        const int pmask = (1 << p.pages.shift) - 1;
+#pragma unroll
+        for (int u = 0; u < PER_THREAD; ++u) {
+          const int j = kt0 + key0 + u * KSTEP;
+          const int32_t blk = sm_pg[(j >> p.pages.shift) - page_lo];
+          const int64_t pj = (static_cast<int64_t>(max(blk, 0)) << p.pages.shift) | (j & pmask);
+          const uint4 kx = *reinterpret_cast<const uint4*>(kbase + pj * kst + dc0 * 16);
+          const uint4 vx = *reinterpret_cast<const uint4*>(vbase + pj * vst + dc0 * 16);
+          kr[u] = blk >= 0 ? kx : make_uint4(0, 0, 0, 0);
+          vr[u] = blk >= 0 ? vx : make_uint4(0, 0, 0, 0);
+        }
+        return;
+      }
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
         const int j = kt0 + key0 + u * KSTEP;
