@@ -346,7 +346,9 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
     op-by-op QK prologue (eager; it needs get_pos(), a host sync), the fused prologue (eager), and the
     fused prologue with one decode step captured in a HIP graph (possible because the fused path has no
     host sync), with torch's logits head and with the fused one (nc_linear + softcap).  Then the
-    C3-shaped Engine.generate in the same modes, the last one also sampling with nc_sample."""
+    C3-shaped Engine.generate in the same modes, the last two also sampling with nc_sample, the last one
+    with the block projections on nc_linear as well (16 rows).  The d20 step's 32 rows keep F.linear for the
+    block projections (nanochat_amd.linear.prefer_for_projection)."""
     from nanochat_amd.engine import KVCache
     from nanochat_amd.gpt import GPTConfig, build_model
     cfg = GPTConfig(sequence_len=2048, vocab_size=32768, n_layer=20, n_head=10, n_kv_head=10, n_embd=1280)
@@ -420,11 +422,15 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
     model3 = build_model(cfg3, dev, compute_dtype=torch.bfloat16, seed=0)
     g3 = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, 32759, (1024,), generator=g3).tolist()
-    for name, fused, use_graph, head_smp in (("op_by_op", False, False, False), ("fused", True, False, False),
-                                             ("fused_graph", True, True, False),
-                                             ("fused_graph_head_sampler", True, True, True)):
+    import nanochat_amd.gpt as gpt_mod
+    for name, fused, use_graph, head_smp, proj in (("op_by_op", False, False, False, False),
+                                                   ("fused", True, False, False, False),
+                                                   ("fused_graph", True, True, False, False),
+                                                   ("fused_graph_head_sampler", True, True, True, False),
+                                                   ("fused_graph_head_sampler_proj", True, True, True, True)):
         model3.fused_qk_prologue = fused
         model3.fused_logits_head = head_smp
+        gpt_mod.SMALL_M_PROJECTIONS = proj   # 16 rows: q/k/v, c_proj and c_fc on nc_linear
         engine = Engine(model3, _Tok(), use_graph=use_graph, fused_sampling=head_smp)
         for _ in engine.generate(prompt, num_samples=16, max_tokens=4, temperature=1.0, seed=0):
             pass  # warm up
@@ -439,6 +445,7 @@ def run_e2e(dev, stream, steps, kps=0, ckps=0):
         out[f"engine_c3_{name}_tokens_per_s"] = round(16 * n / dt, 1)
     model3.fused_qk_prologue = True
     model3.fused_logits_head = True
+    gpt_mod.SMALL_M_PROJECTIONS = True
     out["engine_c3_workload"] = (f"Engine.generate d24 (random init, bf16), 1024-token prompt, 16 samples, {steps} "
                                  "tokens incl. prefill + fan-out; wall clock")
     return out

@@ -256,10 +256,12 @@ int nc_attn_kvcache_rope(const nc_attn_args* args, const nc_qk_prologue* prologu
  * vocabulary size (not the padded row count of W) gives the sliced logits
  * `[..., :vocab_size]` directly.
  *
- * K may be split over workgroups: nc_linear_workspace_bytes() is then
- * non-zero, and the workspace follows the same rule as nc_attn_kvcache's
- * (first NC_WORKSPACE_SYNC_BYTES zero before the first call, left zero by
- * every call).  Results do not depend on the order in which workgroups run.
+ * With few 64-column blocks, K is split: for m <= 32 over the waves of one
+ * workgroup (no workspace), otherwise over workgroups.  In that case
+ * nc_linear_workspace_bytes() is non-zero and the workspace follows the same
+ * rule as nc_attn_kvcache's (first NC_WORKSPACE_SYNC_BYTES zero before the
+ * first call, left zero by every call).  Results do not depend on the order
+ * in which workgroups run.
  * ------------------------------------------------------------------------- */
 typedef struct nc_linear_args {
   const void* x;                 /* (m, k), rows x_stride_m elements apart, 16-byte aligned */

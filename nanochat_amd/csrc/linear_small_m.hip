@@ -22,9 +22,12 @@
 // stream W at 5.5-5.9 TB/s (32 x 32768 x 1280: 15.3 us, the library GEMM
 // 15.1; at M = 16 and M = 1 this kernel is 11-16% faster), and the fused
 // head takes 16.2 us against 26.0 us for the library GEMM plus torch's slice,
-// cast and softcap.  The d20 projections (3-13 MB of W) are latency-bound and
-// the library's single-pass kernels are faster there (4.8 vs 8.5 us at
-// 32 x 1280 x 1280): split K costs two more memory round trips.
+// cast and softcap.  The block projections (3-13 MB of W) are latency-bound:
+// there split K across workgroups costs two more memory round trips, so for
+// m <= 32 the narrow kernel below splits K over the waves of one workgroup
+// instead (32 x 3840 x 1280: 10.3 -> 6.5 us; 16 rows: 4.7-8.4 us, 15-40%
+// below the library GEMM at K <= 2048; at 32 rows, and at K >= 5120, the
+// library is level or faster, as each workgroup then reads all of x from L2).
 //
 // Epilogue: fp32 accumulator -> output dtype (round to nearest even), or,
 // with softcap > 0, the logits head: the accumulator is rounded to the input
@@ -324,6 +327,127 @@ __global__ __launch_bounds__(kLinWaves * kWave) void linear_small_m_kernel(const
   for (int mt = 0; mt < MT; ++mt) lin_store<TC>(p, mt * 16 + lr, col0, sum[mt]);
 }
 
+// x^T operand of chunk c for lane (lr, lq) and m-tile mt: x[mt*16 + lr][c*128 + 32 j + 8 lq, +8)
+// (K % 8 == 0, so an 8-element group is wholly inside or outside K).
+template <int MT>
+__device__ __forceinline__ void lin_load_xb(__amdgpu_buffer_rsrc_t rx, const uint32_t (&x_off)[MT], int k, int lq,
+                                            int c, lin_u4 (&xb)[MT][4]) {
+  const int k0 = c * kLinChunk + 8 * lq;
+  const lin_u4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool in = k0 + 32 * j < k;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const lin_u4 v = __builtin_amdgcn_raw_buffer_load_b128(rx, in ? x_off[mt] + 2u * (k0 + 32 * j) : 0u, 0, 0);
+      xb[mt][j] = in ? v : zero;
+    }
+  }
+}
+
+// Narrow plan (M <= 32 and few 64-column blocks: the decode step's own
+// projections, 3-13 MB of W).  A workgroup owns 16 columns and its KW waves
+// split K among themselves (chunk c goes to wave c % KW), each streaming W
+// and x straight into registers kLinNarrowPD chunks ahead.  The waves' fp32
+// partials meet in LDS and wave 0 adds them in wave order, so the result does
+// not depend on timing, and nothing crosses workgroups: one pass, no
+// workspace, no ticket.  (x is read once per workgroup from L2; at these
+// sizes that costs less than the split plan's two extra memory round trips.)
+constexpr int kLinNarrowPD = 2;
+template <typename TC, int MT, int KW>
+__global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearParams p) {
+  __shared__ lin_f4 red[KW - 1][MT][kWave];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lq = lane / 16;
+  const int lr = lane % 16;
+
+  const int n0 = blockIdx.x * 16;
+  const int rows_in_blk = min(16, p.n - n0);
+  // rows past n read the block's last row, rows past m the last x row: they feed only unstored outputs
+  const int wrow = min(lr, rows_in_blk - 1);
+  const __amdgpu_buffer_rsrc_t rw = lin_rsrc(
+      p.w + static_cast<int64_t>(n0) * p.w_st,
+      static_cast<uint32_t>(2 * (static_cast<int64_t>(rows_in_blk - 1) * p.w_st + p.k)));
+  const __amdgpu_buffer_rsrc_t rx = lin_rsrc(
+      p.x, static_cast<uint32_t>(2 * (static_cast<int64_t>(p.m - 1) * p.x_st + p.k)));
+  const uint32_t w_row_off = 2u * static_cast<uint32_t>(wrow * p.w_st);
+  uint32_t x_off[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) x_off[mt] = 2u * static_cast<uint32_t>(min(mt * 16 + lr, p.m - 1) * p.x_st);
+
+  lin_f4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = lin_f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  lin_u4 wr[kLinNarrowPD][4];
+  lin_u4 xr[kLinNarrowPD][MT][4];
+#pragma unroll
+  for (int s = 0; s < kLinNarrowPD; ++s) {
+    const int c = wave + s * KW;
+    if (c < p.chunks) {
+      lin_load_w(rw, w_row_off, p.k, lq, c, wr[s]);
+      lin_load_xb<MT>(rx, x_off, p.k, lq, c, xr[s]);
+    }
+  }
+  for (int c0 = wave; c0 < p.chunks; c0 += kLinNarrowPD * KW) {
+#pragma unroll
+    for (int s = 0; s < kLinNarrowPD; ++s) {
+      const int c = c0 + s * KW;
+      if (c < p.chunks) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) lin_mfma<TC>::run(wr[s][j], xr[s][mt][j], acc[mt]);
+        }
+        const int cn = c + kLinNarrowPD * KW;
+        if (cn < p.chunks) {
+          lin_load_w(rw, w_row_off, p.k, lq, cn, wr[s]);
+          lin_load_xb<MT>(rx, x_off, p.k, lq, cn, xr[s]);
+        }
+      }
+    }
+  }
+
+  if (wave > 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[wave - 1][mt][lane] = acc[mt];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < KW - 1; ++w) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] += red[w][mt][lane];
+  }
+  const int col0 = n0 + 4 * lq;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) lin_store<TC>(p, mt * 16 + lr, col0, acc[mt]);
+}
+
+template <typename TC, int MT, int KW>
+hipError_t launch_narrow_t(const LinearParams& p, int64_t blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((linear_narrow_kernel<TC, MT, KW>), dim3(static_cast<unsigned>(blocks)), dim3(KW * kWave), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+template <typename TC, int MT>
+hipError_t launch_narrow_m(const LinearParams& p, int64_t blocks, int kw, hipStream_t stream) {
+  switch (kw) {
+    case 16: return launch_narrow_t<TC, MT, 16>(p, blocks, stream);
+    case 8: return launch_narrow_t<TC, MT, 8>(p, blocks, stream);
+    default: return launch_narrow_t<TC, MT, 4>(p, blocks, stream);
+  }
+}
+
+template <typename TC>
+hipError_t launch_narrow(const LinearParams& p, int64_t blocks, int kw, hipStream_t stream) {
+  return p.m > 16 ? launch_narrow_m<TC, 2>(p, blocks, kw, stream) : launch_narrow_m<TC, 1>(p, blocks, kw, stream);
+}
+
 template <typename TC, int MT>
 hipError_t launch_lin_t(const LinearParams& p, int64_t blocks, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(blocks * p.splits));
@@ -350,6 +474,19 @@ LinearPlan plan_linear(int64_t m, int64_t n, int64_t k) {
   pl.chunks = (k + kLinChunk - 1) / kLinChunk;
   // split K until the grid covers every CU about twice (at least one chunk per split)
   int64_t splits = (kLinTargetWG + pl.n_blocks - 1) / pl.n_blocks;
+  if (m <= kLinNarrowMaxM && splits > 1) {
+    // the narrow kernel instead: waves per workgroup doubled from 4 (at most 16, and not past
+    // the chunk count) until the grid holds about kLinNarrowWaves waves
+    const int64_t n16 = (n + 15) / 16;
+    int kw = 4;
+    while (kw < 16 && n16 * kw < kLinNarrowWaves && kw < pl.chunks) kw *= 2;
+    pl.narrow_waves = kw;
+    pl.n_blocks = n16;
+    pl.chunks_per_split = pl.chunks;
+    pl.splits = 1;
+    pl.part_bytes = pl.total_bytes = 0;
+    return pl;
+  }
   splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(splits, pl.chunks), kLinMaxSplits));
   if (pl.n_blocks > kLinMaxTickets) splits = 1;
   pl.chunks_per_split = (pl.chunks + splits - 1) / splits;
@@ -380,6 +517,10 @@ hipError_t launch_linear(const nc_linear_args& a, const LinearPlan& pl, void* wo
   if (pl.splits > 1) {
     p.tickets = static_cast<uint32_t*>(workspace);
     p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + NC_WORKSPACE_SYNC_BYTES);
+  }
+  if (pl.narrow_waves > 0) {
+    return a.dtype == NC_DTYPE_BF16 ? launch_narrow<bf16>(p, pl.n_blocks, pl.narrow_waves, stream)
+                                    : launch_narrow<f16>(p, pl.n_blocks, pl.narrow_waves, stream);
   }
   return a.dtype == NC_DTYPE_BF16 ? launch_lin_m<bf16>(p, pl.n_blocks, stream)
                                   : launch_lin_m<f16>(p, pl.n_blocks, stream);

@@ -97,6 +97,13 @@ constexpr int64_t kLinMaxSplits = NC_LIN_MAX_SPLITS;
 // Column blocks that can take split-K tickets (one uint32 each in the sync region).
 constexpr int64_t kLinMaxTickets = NC_WORKSPACE_SYNC_BYTES / 4;
 constexpr int64_t kLinMaxM = 64;
+// Narrow plan: M <= kLinNarrowMaxM with few column blocks; waves per workgroup
+// sized so the grid holds about kLinNarrowWaves waves.
+constexpr int64_t kLinNarrowMaxM = 32;
+#ifndef NC_LIN_NARROW_WAVES
+#define NC_LIN_NARROW_WAVES 1024
+#endif
+constexpr int64_t kLinNarrowWaves = NC_LIN_NARROW_WAVES;
 // Row strides (elements) the kernel's 32-bit buffer offsets cover.
 constexpr int64_t kLinMaxStride = int64_t(1) << 24;
 
@@ -106,6 +113,7 @@ struct LinearPlan {
   int64_t chunks;         // ceil(k / 128)
   int64_t chunks_per_split;
   int64_t splits;         // > 1: partials summed by the last workgroup of a block
+  int narrow_waves;       // > 0: the narrow kernel (16 columns per workgroup, K split over this many waves)
   size_t part_bytes, total_bytes;
 };
 

@@ -28,7 +28,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import linear as head_kernel
+from . import linear as small_m
 from .common import COMPUTE_DTYPE
 from .flash_attention import flash_attn
 
@@ -47,6 +47,12 @@ class GPTConfig:
 def rms(x):
     """Parameter-free RMS norm over the last dimension."""
     return F.rms_norm(x, (x.size(-1),))
+
+
+# Decode-sized block projections (at most 16 rows, K <= 2048, inference) run on the library's
+# small-M kernel where it measured faster than the library GEMM (nanochat_amd.linear.
+# prefer_for_projection); False keeps F.linear for every projection.
+SMALL_M_PROJECTIONS = True
 
 
 class CastLinear(nn.Linear):
@@ -69,7 +75,10 @@ class CastLinear(nn.Linear):
         return cached[1]
 
     def forward(self, x):
-        return F.linear(x, self.weight_as(x.dtype))
+        w = self.weight_as(x.dtype)
+        if SMALL_M_PROJECTIONS and small_m.prefer_for_projection(x, w):
+            return small_m.linear(x, w)
+        return F.linear(x, w)
 
 
 def carries_value_embedding(layer, n_layer):
@@ -146,7 +155,11 @@ class CausalSelfAttention(nn.Module):
     def forward(self, x, ve, cos_sin, window_size, kv_cache):
         B, T, _ = x.size()
         if isinstance(cos_sin, FusedRope) and cos_sin.fuse_qkv and x.dtype in (torch.bfloat16, torch.float16):
-            qkv = F.linear(x, self.qkv_weight(x.dtype))
+            w = self.qkv_weight(x.dtype)
+            if SMALL_M_PROJECTIONS and small_m.prefer_for_projection(x, w):
+                qkv = small_m.linear(x, w)
+            else:
+                qkv = F.linear(x, w)
             nq, nk = self.n_head * self.head_dim, self.n_kv_head * self.head_dim
             q = qkv[..., :nq].view(B, T, self.n_head, self.head_dim)
             k = qkv[..., nq:nq + nk].view(B, T, self.n_kv_head, self.head_dim)
@@ -341,8 +354,8 @@ class GPT(nn.Module):
         softcap = 15
         if self.fused_logits_head and x.is_cuda:
             w = self.lm_head.weight_as(x.dtype)
-            if head_kernel.supported(x, w):
-                return head_kernel.logits_head(x, w, self.config.vocab_size, softcap)
+            if small_m.supported(x, w):
+                return small_m.logits_head(x, w, self.config.vocab_size, softcap)
         logits = self.lm_head(x)[..., :self.config.vocab_size].float()
         return softcap * torch.tanh(logits / softcap)
 

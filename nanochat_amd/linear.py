@@ -36,6 +36,24 @@ def supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
     return 1 <= m <= MAX_M
 
 
+# Block projections of a decode step go to the kernel only where it measured faster than the
+# library GEMM (MI355X, HIP graph replays, bf16, weights streamed from HBM): at most 16 rows and
+# K <= 2048, e.g. 16 x 4608 x 1536 in 8.0 vs 9.6 us and 16 x 1280 x 1280 in 4.7 vs 6.3 us.  At 32
+# rows the two are level or the library is faster (32 x 5120 x 1280: 10.8 vs 8.7 us), and so it is
+# at K >= 5120 (16 x 1280 x 5120: 12.4 vs 9.4 us); tiny weights are launch-bound either way.
+PROJ_MAX_M, PROJ_MAX_K, PROJ_MIN_DIM = 16, 2048, 512
+
+
+def prefer_for_projection(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """True if F.linear(x, weight) should run on the kernel: a supported, inference-only
+    (no autograd) shape in the region where it beats the library GEMM."""
+    if torch.is_grad_enabled() or not supported(x, weight):
+        return False
+    n, k = weight.shape
+    m = x.numel() // k
+    return m <= PROJ_MAX_M and PROJ_MIN_DIM <= k <= PROJ_MAX_K and n >= PROJ_MIN_DIM
+
+
 def _rows(t: torch.Tensor, cols: int) -> torch.Tensor:
     """t as an (rows, cols) matrix with unit column stride, without copying when possible."""
     t2 = t.reshape(-1, cols)

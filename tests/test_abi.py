@@ -157,16 +157,22 @@ def test_invalid_arguments_are_rejected_before_launch():
 def test_linear_plan_splits_k_to_fill_the_gpu():
     lib = _ext.lib()
     sync = _ext.NC_WORKSPACE_SYNC_BYTES
-    # (m, n, k) -> splits: 64-column blocks x splits reaches about 512 workgroups, with at least
-    # one 128-wide chunk of k per split and at most 4 splits; partials are 64 columns x m_tiles x
-    # 16 rows fp32 per (block, split)
-    for (m, n, k), splits in {(32, 1280, 1280): 4, (32, 1280, 5120): 4, (32, 5120, 1280): 4,
-                              (16, 1536, 6144): 4, (1, 1280, 1280): 4, (64, 1280, 1280): 4,
-                              (32, 640, 896): 4, (32, 20000, 1280): 2, (8, 64, 256): 2}.items():
+    # (m, n, k) -> splits, for m > 32: 64-column blocks x splits reaches about 512 workgroups, with
+    # at least one 128-wide chunk of k per split and at most 4 splits; partials are 64 columns x
+    # m_tiles x 16 rows fp32 per (block, split)
+    for (m, n, k), splits in {(64, 1280, 1280): 4, (64, 1280, 5120): 4, (48, 5120, 1280): 4,
+                              (33, 1536, 6144): 4, (48, 640, 896): 4, (33, 20000, 1280): 2,
+                              (64, 64, 256): 2}.items():
         m_tiles, n_blocks = (m + 15) // 16, (n + 63) // 64
         assert lib.nc_linear_workspace_bytes(m, n, k) == sync + n_blocks * splits * 64 * m_tiles * 64, (m, n, k)
+    # m <= 32 where the 64-column plan would split K: the narrow kernel (K split over the waves of
+    # one workgroup, summed in LDS), no workspace
+    for m, n, k in [(32, 1280, 1280), (32, 1280, 5120), (32, 5120, 1280), (16, 1536, 6144), (1, 1280, 1280),
+                    (32, 640, 896), (32, 20000, 1280), (8, 64, 256)]:
+        assert lib.nc_linear_workspace_bytes(m, n, k) == 0, (m, n, k)
     # no split: at least 512 column blocks (lm_head)
     assert lib.nc_linear_workspace_bytes(32, 32768, 1280) == 0
+    assert lib.nc_linear_workspace_bytes(64, 32768, 1280) == 0
     assert lib.nc_linear_workspace_bytes(32, 65536, 2048) == 0
     assert lib.nc_linear_workspace_bytes(0, 16, 16) == 0
 
@@ -201,9 +207,9 @@ def test_linear_rejects_bad_arguments_before_launch():
     a.x = fake + 8
     assert lib.nc_linear(ctypes.byref(a), None) == 5
     a.x = fake
-    a.n, a.k, a.w_stride_n, a.x_stride_m, a.y_stride_m = 1280, 1280, 1280, 1280, 1280
+    a.m, a.n, a.k, a.w_stride_n, a.x_stride_m, a.y_stride_m = 64, 1280, 1280, 1280, 1280, 1280
     assert lib.nc_linear(ctypes.byref(a), None) == 6          # K split: needs a workspace
-    a.workspace, a.workspace_bytes = fake, lib.nc_linear_workspace_bytes(32, 1280, 1280) - 16
+    a.workspace, a.workspace_bytes = fake, lib.nc_linear_workspace_bytes(64, 1280, 1280) - 16
     assert lib.nc_linear(ctypes.byref(a), None) == 6
 
 

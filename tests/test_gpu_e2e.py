@@ -312,3 +312,40 @@ def test_fused_qkv_projection_in_the_model():
         assert float((a - b).abs().max()) <= 2e-2 * float(b.abs().max()) + 1e-3
     assert torch.equal(outs[0][1].cache_seqlens, outs[1][1].cache_seqlens)
     assert float((outs[0][1].k_cache.float() - outs[1][1].k_cache.float()).abs().max()) <= 0.05
+
+
+def test_small_m_projections_in_the_model(monkeypatch):
+    """A bf16 decode step with the block projections on the small-M kernel (at most 16 rows,
+    K <= 2048) equals the library GEMM path up to summation order: logits and appended cache."""
+    from nanochat_amd import linear as small_m
+    cfg = gpt.GPTConfig(sequence_len=256, vocab_size=5000, n_layer=2, n_head=4, n_kv_head=4, n_embd=512)
+    model = gpt.build_model(cfg, DEV, compute_dtype=torch.bfloat16, seed=6)
+    for blk in model.transformer.h:
+        torch.nn.init.normal_(blk.attn.c_proj.weight, std=0.02)
+        torch.nn.init.normal_(blk.mlp.c_proj.weight, std=0.02)
+    g = torch.Generator().manual_seed(6)
+    prompt = torch.randint(0, 5000, (1, 24), generator=g).to(DEV)
+    step_ids = torch.randint(0, 5000, (8, 1), generator=g).to(DEV)
+    calls = []
+    real = small_m.linear
+    monkeypatch.setattr(small_m, "linear", lambda x, w: calls.append(tuple(w.shape)) or real(x, w))
+    outs = []
+    for on in (True, False):
+        monkeypatch.setattr(gpt, "SMALL_M_PROJECTIONS", on)
+        calls.clear()
+        kv = KVCache(batch_size=8, num_heads=4, seq_len=40, head_dim=128, num_layers=2, device=DEV,
+                     dtype=torch.bfloat16)
+        pre = KVCache(batch_size=1, num_heads=4, seq_len=24, head_dim=128, num_layers=2, device=DEV,
+                      dtype=torch.bfloat16)
+        with torch.inference_mode():
+            model.forward(prompt, kv_cache=pre)
+            kv.prefill(pre)
+            step_calls = len(calls)
+            logits = [model.forward(step_ids, kv_cache=kv)[:, -1, :].float() for _ in range(2)]
+        outs.append((logits, kv, len(calls) - step_calls))
+    # per layer and step: q/k/v (one GEMM), attention c_proj, MLP c_fc and c_proj
+    assert outs[0][2] == 2 * 2 * 4 and outs[1][2] == 0
+    for a, b in zip(outs[0][0], outs[1][0]):
+        assert float((a - b).abs().max()) <= 2e-2 * float(b.abs().max()) + 1e-3
+    assert torch.equal(outs[0][1].cache_seqlens, outs[1][1].cache_seqlens)
+    assert float((outs[0][1].k_cache.float() - outs[1][1].k_cache.float()).abs().max()) <= 0.05

@@ -33,6 +33,8 @@ def _int_operands(seed, m, n, k, dtype):
 @pytest.mark.parametrize("m,n,k", [
     (1, 1, 8), (1, 10, 24), (5, 100, 136), (16, 16, 128), (17, 33, 264), (32, 1280, 1280),
     (32, 5120, 1280), (32, 1280, 5120), (33, 96, 2048), (48, 200, 640), (64, 1280, 1280), (16, 1536, 6144),
+    # narrow plan (m <= 32): 8 waves per workgroup, waves with no chunk, a partial last chunk
+    (32, 3840, 1280), (9, 2100, 520), (32, 136, 4104), (2, 24, 392),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_linear_exact_on_integer_operands(m, n, k, dtype):
@@ -129,8 +131,8 @@ def test_logits_head_epilogue_every_bf16_value():
 def test_split_counters_return_to_zero_between_linear_and_attention():
     from nanochat_amd.flash_attention import flash_attn
     g = gen(21)
-    wk = randn((1280, 5120), g, torch.bfloat16).to(DEV)   # K split over 7 workgroups per column tile
-    xk = randn((32, 5120), g, torch.bfloat16).to(DEV)
+    wk = randn((1280, 5120), g, torch.bfloat16).to(DEV)   # K split over 4 workgroups per column block
+    xk = randn((64, 5120), g, torch.bfloat16).to(DEV)
     first = linear(xk, wk)
     q = randn((8, 1, 16, 128), g, torch.bfloat16).to(DEV)
     kc = randn((8, 4096, 4, 128), g, torch.bfloat16).to(DEV)
@@ -155,7 +157,7 @@ def test_supported_and_rejections():
         linear(torch.zeros((MAX_M + 1, 64), dtype=torch.bfloat16, device=DEV), w)
     # the C ABI rejects a missing workspace when K is split
     L = _ext.lib()
-    m, n, k = 32, 1280, 1280
+    m, n, k = 64, 1280, 1280
     assert L.nc_linear_workspace_bytes(m, n, k) > 0
     x = torch.zeros((m, k), dtype=torch.bfloat16, device=DEV)
     ww = torch.zeros((n, k), dtype=torch.bfloat16, device=DEV)
