@@ -354,9 +354,9 @@ __device__ __forceinline__ void lin_load_xb(__amdgpu_buffer_rsrc_t rx, const uin
 // workspace, no ticket.  (x is read once per workgroup from L2; at these
 // sizes that costs less than the split plan's two extra memory round trips.)
 constexpr int kLinNarrowPD = 2;
-template <typename TC, int MT, int KW>
+template <typename TC, int MT, int KW, int NT>
 __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearParams p) {
-  __shared__ lin_f4 red[KW - 1][MT][kWave];
+  __shared__ lin_f4 red[KW - 1][NT][MT][kWave];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -364,31 +364,38 @@ __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearP
   const int lq = lane / 16;
   const int lr = lane % 16;
 
-  const int n0 = blockIdx.x * 16;
-  const int rows_in_blk = min(16, p.n - n0);
+  // the workgroup's 16 * NT columns; each wave runs all NT column tiles on its chunks, so one x
+  // load feeds NT MFMAs
+  const int n0 = blockIdx.x * 16 * NT;
+  const int rows_in_blk = min(16 * NT, p.n - n0);
   // rows past n read the block's last row, rows past m the last x row: they feed only unstored outputs
-  const int wrow = min(lr, rows_in_blk - 1);
   const __amdgpu_buffer_rsrc_t rw = lin_rsrc(
       p.w + static_cast<int64_t>(n0) * p.w_st,
       static_cast<uint32_t>(2 * (static_cast<int64_t>(rows_in_blk - 1) * p.w_st + p.k)));
   const __amdgpu_buffer_rsrc_t rx = lin_rsrc(
       p.x, static_cast<uint32_t>(2 * (static_cast<int64_t>(p.m - 1) * p.x_st + p.k)));
-  const uint32_t w_row_off = 2u * static_cast<uint32_t>(wrow * p.w_st);
+  uint32_t w_row_off[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) w_row_off[nt] = 2u * static_cast<uint32_t>(min(16 * nt + lr, rows_in_blk - 1) * p.w_st);
   uint32_t x_off[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) x_off[mt] = 2u * static_cast<uint32_t>(min(mt * 16 + lr, p.m - 1) * p.x_st);
 
-  lin_f4 acc[MT];
+  lin_f4 acc[NT][MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = lin_f4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = lin_f4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 
-  lin_u4 wr[kLinNarrowPD][4];
+  lin_u4 wr[kLinNarrowPD][NT][4];
   lin_u4 xr[kLinNarrowPD][MT][4];
 #pragma unroll
   for (int s = 0; s < kLinNarrowPD; ++s) {
     const int c = wave + s * KW;
     if (c < p.chunks) {
-      lin_load_w(rw, w_row_off, p.k, lq, c, wr[s]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) lin_load_w(rw, w_row_off[nt], p.k, lq, c, wr[s][nt]);
       lin_load_xb<MT>(rx, x_off, p.k, lq, c, xr[s]);
     }
   }
@@ -400,11 +407,15 @@ __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearP
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt) lin_mfma<TC>::run(wr[s][j], xr[s][mt][j], acc[mt]);
+          for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) lin_mfma<TC>::run(wr[s][nt][j], xr[s][mt][j], acc[nt][mt]);
+          }
         }
         const int cn = c + kLinNarrowPD * KW;
         if (cn < p.chunks) {
-          lin_load_w(rw, w_row_off, p.k, lq, cn, wr[s]);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) lin_load_w(rw, w_row_off[nt], p.k, lq, cn, wr[s][nt]);
           lin_load_xb<MT>(rx, x_off, p.k, lq, cn, xr[s]);
         }
       }
@@ -413,39 +424,55 @@ __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearP
 
   if (wave > 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) red[wave - 1][mt][lane] = acc[mt];
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[wave - 1][nt][mt][lane] = acc[nt][mt];
+    }
   }
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int w = 0; w < KW - 1; ++w) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] += red[w][mt][lane];
-  }
-  const int col0 = n0 + 4 * lq;
+    for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) lin_store<TC>(p, mt * 16 + lr, col0, acc[mt]);
+      for (int mt = 0; mt < MT; ++mt) acc[nt][mt] += red[w][nt][mt][lane];
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int col0 = n0 + 16 * nt + 4 * lq;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) lin_store<TC>(p, mt * 16 + lr, col0, acc[nt][mt]);
+  }
 }
 
-template <typename TC, int MT, int KW>
+template <typename TC, int MT, int KW, int NT>
 hipError_t launch_narrow_t(const LinearParams& p, int64_t blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_narrow_kernel<TC, MT, KW>), dim3(static_cast<unsigned>(blocks)), dim3(KW * kWave), 0,
-                     stream, p);
+  hipLaunchKernelGGL((linear_narrow_kernel<TC, MT, KW, NT>), dim3(static_cast<unsigned>(blocks)), dim3(KW * kWave),
+                     0, stream, p);
   return hipGetLastError();
 }
 
-template <typename TC, int MT>
-hipError_t launch_narrow_m(const LinearParams& p, int64_t blocks, int kw, hipStream_t stream) {
-  switch (kw) {
-    case 16: return launch_narrow_t<TC, MT, 16>(p, blocks, stream);
-    case 8: return launch_narrow_t<TC, MT, 8>(p, blocks, stream);
-    default: return launch_narrow_t<TC, MT, 4>(p, blocks, stream);
-  }
-}
-
+// tiles = 1: one 16-column tile per wave, 4-16 waves; tiles = 2 (16 < m <= 32, wide n): two tiles per
+// wave sharing each x load, 4-8 waves (VGPRs)
 template <typename TC>
-hipError_t launch_narrow(const LinearParams& p, int64_t blocks, int kw, hipStream_t stream) {
-  return p.m > 16 ? launch_narrow_m<TC, 2>(p, blocks, kw, stream) : launch_narrow_m<TC, 1>(p, blocks, kw, stream);
+hipError_t launch_narrow(const LinearParams& p, int64_t blocks, int kw, int tiles, hipStream_t stream) {
+  if (p.m > 16) {
+    if (tiles == 2) {
+      return kw >= 8 ? launch_narrow_t<TC, 2, 8, 2>(p, blocks, stream) : launch_narrow_t<TC, 2, 4, 2>(p, blocks, stream);
+    }
+    switch (kw) {
+      case 16: return launch_narrow_t<TC, 2, 16, 1>(p, blocks, stream);
+      case 8: return launch_narrow_t<TC, 2, 8, 1>(p, blocks, stream);
+      default: return launch_narrow_t<TC, 2, 4, 1>(p, blocks, stream);
+    }
+  }
+  switch (kw) {
+    case 16: return launch_narrow_t<TC, 1, 16, 1>(p, blocks, stream);
+    case 8: return launch_narrow_t<TC, 1, 8, 1>(p, blocks, stream);
+    default: return launch_narrow_t<TC, 1, 4, 1>(p, blocks, stream);
+  }
 }
 
 template <typename TC, int MT>
@@ -475,13 +502,20 @@ LinearPlan plan_linear(int64_t m, int64_t n, int64_t k) {
   // split K until the grid covers every CU about twice (at least one chunk per split)
   int64_t splits = (kLinTargetWG + pl.n_blocks - 1) / pl.n_blocks;
   if (m <= kLinNarrowMaxM && splits > 1) {
-    // the narrow kernel instead: waves per workgroup doubled from 4 (at most 16, and not past
-    // the chunk count) until the grid holds about kLinNarrowWaves waves
-    const int64_t n16 = (n + 15) / 16;
+    // the narrow kernel instead.  Two column tiles per wave for m > 16 when 8-wave workgroups of
+    // 32 columns already give about kLinNarrowWaves waves (x loads then feed twice the MFMAs;
+    // with fewer columns the lost workgroups cost more: 32 x 3840 x 1280 6.5 us at one tile,
+    // 8.3 at two; 32 x 5120 x 1280 10.8 and 8.9).  Waves per workgroup doubled from 4 (at most
+    // 16, 8 with two tiles, and not past the chunk count) until the grid holds about that many.
+    const int tiles = (m > 16 && (n + 31) / 32 * 8 >= kLinNarrowWaves) ? 2 : 1;
+    const int64_t cols = 16 * tiles;
+    const int64_t nb = (n + cols - 1) / cols;
+    const int kw_max = tiles == 2 ? 8 : 16;
     int kw = 4;
-    while (kw < 16 && n16 * kw < kLinNarrowWaves && kw < pl.chunks) kw *= 2;
+    while (kw < kw_max && nb * kw < kLinNarrowWaves && kw < pl.chunks) kw *= 2;
     pl.narrow_waves = kw;
-    pl.n_blocks = n16;
+    pl.narrow_tiles = tiles;
+    pl.n_blocks = nb;
     pl.chunks_per_split = pl.chunks;
     pl.splits = 1;
     pl.part_bytes = pl.total_bytes = 0;
@@ -519,8 +553,8 @@ hipError_t launch_linear(const nc_linear_args& a, const LinearPlan& pl, void* wo
     p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + NC_WORKSPACE_SYNC_BYTES);
   }
   if (pl.narrow_waves > 0) {
-    return a.dtype == NC_DTYPE_BF16 ? launch_narrow<bf16>(p, pl.n_blocks, pl.narrow_waves, stream)
-                                    : launch_narrow<f16>(p, pl.n_blocks, pl.narrow_waves, stream);
+    return a.dtype == NC_DTYPE_BF16 ? launch_narrow<bf16>(p, pl.n_blocks, pl.narrow_waves, pl.narrow_tiles, stream)
+                                    : launch_narrow<f16>(p, pl.n_blocks, pl.narrow_waves, pl.narrow_tiles, stream);
   }
   return a.dtype == NC_DTYPE_BF16 ? launch_lin_m<bf16>(p, pl.n_blocks, stream)
                                   : launch_lin_m<f16>(p, pl.n_blocks, stream);

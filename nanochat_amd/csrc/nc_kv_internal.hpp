@@ -104,6 +104,7 @@ constexpr int64_t kLinNarrowMaxM = 32;
 #define NC_LIN_NARROW_WAVES 1024
 #endif
 constexpr int64_t kLinNarrowWaves = NC_LIN_NARROW_WAVES;
+
 // Row strides (elements) the kernel's 32-bit buffer offsets cover.
 constexpr int64_t kLinMaxStride = int64_t(1) << 24;
 
@@ -113,7 +114,8 @@ struct LinearPlan {
   int64_t chunks;         // ceil(k / 128)
   int64_t chunks_per_split;
   int64_t splits;         // > 1: partials summed by the last workgroup of a block
-  int narrow_waves;       // > 0: the narrow kernel (16 columns per workgroup, K split over this many waves)
+  int narrow_waves;       // > 0: the narrow kernel (16 * narrow_tiles columns per workgroup, K split over this many waves)
+  int narrow_tiles;       // 16-column MFMA tiles per wave of the narrow kernel (1 or 2)
   size_t part_bytes, total_bytes;
 };
 

@@ -35,6 +35,8 @@ def _int_operands(seed, m, n, k, dtype):
     (32, 5120, 1280), (32, 1280, 5120), (33, 96, 2048), (48, 200, 640), (64, 1280, 1280), (16, 1536, 6144),
     # narrow plan (m <= 32): 8 waves per workgroup, waves with no chunk, a partial last chunk
     (32, 3840, 1280), (9, 2100, 520), (32, 136, 4104), (2, 24, 392),
+    # narrow plan with two column tiles per wave (m > 16, wide n), ragged last block
+    (20, 4100, 264), (32, 6144, 1536),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_linear_exact_on_integer_operands(m, n, k, dtype):
