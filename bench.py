@@ -577,9 +577,21 @@ def run_head(dev, stream, steps, kps=0, ckps=0):
             "nc_top50_us": timed(lambda: sample_with_uniforms(logits, u, 0.8, 50)),
             "torch_top50_us": timed(torch_top50),
         }
+        # block projections (gpt.py:87-89,125,136-138) of d24 at 16 rows (C3's samples) and d20 at 32 rows: one
+        # call per layer's weight, 20 distinct weights per graph pass so W streams from HBM; us per call
+        for rows, shapes, tag in ((16, ((4608, 1536), (1536, 1536), (6144, 1536), (1536, 6144)), "d24_m16"),
+                                  (32, ((3840, 1280), (1280, 1280), (5120, 1280), (1280, 5120)), "d20_m32")):
+            for n, k in shapes:
+                ws = [(torch.randn(n, k, device=dev, generator=g) * k ** -0.5).bfloat16() for _ in range(20)]
+                xp = torch.randn(rows, 1, k, device=dev, generator=g).bfloat16()
+                key = f"proj_{tag}_{n}x{k}"
+                res[key + "_nc_us"] = round(timed(lambda: [linear(xp, wi) for wi in ws]) / 20, 2)
+                res[key + "_torch_us"] = round(timed(lambda: [F.linear(xp, wi) for wi in ws]) / 20, 2)
+                del ws
     head_bytes = V * C * 2 + B * C * 2 + B * V * 4
     return {"config": "head", "workload": f"d20 logits head and sampler, B={B}, vocab {V}, K={C}, bf16; "
-                                          f"{steps} calls per graph", **res,
+                                          f"{steps} calls per graph; block projections (m x n x k, 20 weights "
+                                          f"per pass)", **res,
             "fused_head_bytes_per_call": head_bytes,
             "fused_head_TBps": round(head_bytes / (res["fused_head_us"] * 1e-6) / 1e12, 3)}
 
