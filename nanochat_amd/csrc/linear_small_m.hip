@@ -365,8 +365,13 @@ __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearP
   const int lr = lane % 16;
 
   // the workgroup's 16 * NT columns; each wave runs all NT column tiles on its chunks, so one x
-  // load feeds NT MFMAs
-  const int n0 = blockIdx.x * 16 * NT;
+  // load feeds NT MFMAs.  With splits > 1 (long K, few column blocks) the workgroup takes chunks
+  // [split * chunks_per_split, +chunks_per_split) of its column block.
+  const int blk = static_cast<int>(blockIdx.x) / p.splits;
+  const int split = static_cast<int>(blockIdx.x) - blk * p.splits;
+  const int c_begin = split * p.chunks_per_split;
+  const int c_end = min(p.chunks, c_begin + p.chunks_per_split);
+  const int n0 = blk * 16 * NT;
   const int rows_in_blk = min(16 * NT, p.n - n0);
   // rows past n read the block's last row, rows past m the last x row: they feed only unstored outputs
   const __amdgpu_buffer_rsrc_t rw = lin_rsrc(
@@ -392,18 +397,18 @@ __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearP
   lin_u4 xr[kLinNarrowPD][MT][4];
 #pragma unroll
   for (int s = 0; s < kLinNarrowPD; ++s) {
-    const int c = wave + s * KW;
-    if (c < p.chunks) {
+    const int c = c_begin + wave + s * KW;
+    if (c < c_end) {
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) lin_load_w(rw, w_row_off[nt], p.k, lq, c, wr[s][nt]);
       lin_load_xb<MT>(rx, x_off, p.k, lq, c, xr[s]);
     }
   }
-  for (int c0 = wave; c0 < p.chunks; c0 += kLinNarrowPD * KW) {
+  for (int c0 = c_begin + wave; c0 < c_end; c0 += kLinNarrowPD * KW) {
 #pragma unroll
     for (int s = 0; s < kLinNarrowPD; ++s) {
       const int c = c0 + s * KW;
-      if (c < p.chunks) {
+      if (c < c_end) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
 #pragma unroll
@@ -413,7 +418,7 @@ __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearP
           }
         }
         const int cn = c + kLinNarrowPD * KW;
-        if (cn < p.chunks) {
+        if (cn < c_end) {
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) lin_load_w(rw, w_row_off[nt], p.k, lq, cn, wr[s][nt]);
           lin_load_xb<MT>(rx, x_off, p.k, lq, cn, xr[s]);
@@ -439,6 +444,43 @@ __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearP
       for (int mt = 0; mt < MT; ++mt) acc[nt][mt] += red[w][nt][mt][lane];
     }
   }
+  if (p.splits > 1) {
+    // split K across workgroups as well: wave 0 publishes the workgroup's partial with coherent
+    // stores, waits for them, and takes a ticket; the last split sums the partials in split order
+    constexpr int64_t slot = static_cast<int64_t>(NT) * MT * kWave * 4;
+    float* mine = p.part + (static_cast<int64_t>(blk) * p.splits + split) * slot + lane * 4;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) lin_coherent_store(mine + (nt * MT + mt) * kWave * 4 + r, acc[nt][mt][r]);
+      }
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the wave's partial stores have completed
+    uint32_t tk = 0;
+    if (lane == 0) tk = __hip_atomic_fetch_add(p.tickets + blk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    tk = __shfl(tk, 0);
+    if (tk + 1 != static_cast<uint32_t>(p.splits)) return;
+    if (lane == 0) __hip_atomic_store(p.tickets + blk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __asm__ volatile("" ::: "memory");
+    const float* src_part = p.part + static_cast<int64_t>(blk) * p.splits * slot + lane * 4;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = lin_f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    for (int sp = 0; sp < p.splits; ++sp) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[nt][mt][r] += lin_coherent_load(src_part + sp * slot + (nt * MT + mt) * kWave * 4 + r);
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int col0 = n0 + 16 * nt + 4 * lq;
@@ -449,8 +491,8 @@ __global__ __launch_bounds__(KW * kWave) void linear_narrow_kernel(const LinearP
 
 template <typename TC, int MT, int KW, int NT>
 hipError_t launch_narrow_t(const LinearParams& p, int64_t blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((linear_narrow_kernel<TC, MT, KW, NT>), dim3(static_cast<unsigned>(blocks)), dim3(KW * kWave),
-                     0, stream, p);
+  hipLaunchKernelGGL((linear_narrow_kernel<TC, MT, KW, NT>), dim3(static_cast<unsigned>(blocks * p.splits)),
+                     dim3(KW * kWave), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -516,9 +558,15 @@ LinearPlan plan_linear(int64_t m, int64_t n, int64_t k) {
     pl.narrow_waves = kw;
     pl.narrow_tiles = tiles;
     pl.n_blocks = nb;
-    pl.chunks_per_split = pl.chunks;
-    pl.splits = 1;
-    pl.part_bytes = pl.total_bytes = 0;
+    // long K with fewer column blocks than CUs: K split over 2-4 workgroups as well, while each
+    // split keeps at least one chunk per wave
+    int64_t ns = 1;
+    while (ns < kLinMaxSplits && nb * ns < kLinNarrowMinBlocks && pl.chunks >= 2 * ns * kw) ns *= 2;
+    pl.chunks_per_split = (pl.chunks + ns - 1) / ns;
+    pl.splits = (pl.chunks + pl.chunks_per_split - 1) / pl.chunks_per_split;
+    pl.part_bytes = pl.splits > 1 ? static_cast<size_t>(nb) * pl.splits * tiles * pl.m_tiles * kWave * 4 * sizeof(float)
+                                  : 0;
+    pl.total_bytes = pl.splits > 1 ? NC_WORKSPACE_SYNC_BYTES + pl.part_bytes : 0;
     return pl;
   }
   splits = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(splits, pl.chunks), kLinMaxSplits));

@@ -104,6 +104,8 @@ constexpr int64_t kLinNarrowMaxM = 32;
 #define NC_LIN_NARROW_WAVES 1024
 #endif
 constexpr int64_t kLinNarrowWaves = NC_LIN_NARROW_WAVES;
+// narrow plans with fewer column blocks than this split long K across workgroups too
+constexpr int64_t kLinNarrowMinBlocks = 256;
 
 // Row strides (elements) the kernel's 32-bit buffer offsets cover.
 constexpr int64_t kLinMaxStride = int64_t(1) << 24;

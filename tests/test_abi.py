@@ -166,10 +166,17 @@ def test_linear_plan_splits_k_to_fill_the_gpu():
         m_tiles, n_blocks = (m + 15) // 16, (n + 63) // 64
         assert lib.nc_linear_workspace_bytes(m, n, k) == sync + n_blocks * splits * 64 * m_tiles * 64, (m, n, k)
     # m <= 32 where the 64-column plan would split K: the narrow kernel (K split over the waves of
-    # one workgroup, summed in LDS), no workspace
-    for m, n, k in [(32, 1280, 1280), (32, 1280, 5120), (32, 5120, 1280), (16, 1536, 6144), (1, 1280, 1280),
-                    (32, 640, 896), (32, 20000, 1280), (8, 64, 256)]:
+    # one workgroup, summed in LDS), no workspace ...
+    for m, n, k in [(32, 1280, 1280), (32, 5120, 1280), (1, 1280, 1280), (32, 640, 896), (32, 20000, 1280),
+                    (8, 64, 256), (16, 1536, 1536)]:
         assert lib.nc_linear_workspace_bytes(m, n, k) == 0, (m, n, k)
+    # ... unless K is long and there are fewer than 256 blocks of 16 columns: then K is split over 2
+    # workgroups as well (at least one 128-wide chunk per wave and split; 16 waves here), partials of
+    # 64 lanes x m_tiles x 4 fp32 per (block, split)
+    for (m, n, k), (blocks, splits) in {(32, 1280, 5120): (80, 2), (16, 1536, 6144): (96, 2),
+                                        (32, 136, 4104): (9, 2)}.items():
+        m_tiles = (m + 15) // 16
+        assert lib.nc_linear_workspace_bytes(m, n, k) == sync + blocks * splits * m_tiles * 64 * 4 * 4, (m, n, k)
     # no split: at least 512 column blocks (lm_head)
     assert lib.nc_linear_workspace_bytes(32, 32768, 1280) == 0
     assert lib.nc_linear_workspace_bytes(64, 32768, 1280) == 0

@@ -136,6 +136,7 @@ def test_split_counters_return_to_zero_between_linear_and_attention():
     wk = randn((1280, 5120), g, torch.bfloat16).to(DEV)   # K split over 4 workgroups per column block
     xk = randn((64, 5120), g, torch.bfloat16).to(DEV)
     first = linear(xk, wk)
+    first32 = linear(xk[:32], wk)   # narrow kernel, K split over 2 workgroups per 16 columns
     q = randn((8, 1, 16, 128), g, torch.bfloat16).to(DEV)
     kc = randn((8, 4096, 4, 128), g, torch.bfloat16).to(DEV)
     vc = randn((8, 4096, 4, 128), g, torch.bfloat16).to(DEV)
@@ -143,6 +144,7 @@ def test_split_counters_return_to_zero_between_linear_and_attention():
     for _ in range(3):
         flash_attn.flash_attn_with_kvcache(q, kc, vc, cache_seqlens=sl, causal=True)
         assert torch.equal(bits(linear(xk, wk)), bits(first))
+        assert torch.equal(bits(linear(xk[:32], wk)), bits(first32))
     torch.cuda.synchronize()
     for buf in list(_ext._workspaces.values()):
         assert int(buf[:_ext.NC_WORKSPACE_SYNC_BYTES].count_nonzero()) == 0
