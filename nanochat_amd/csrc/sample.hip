@@ -13,8 +13,8 @@
 // 0 and sets NC_DEVERR_SAMPLE (torch.multinomial raises for such a row).
 //
 // Top-k: the k-th largest value is found by a radix select over the
-// order-preserving 32-bit key of each logit (4 passes of 8 bits, histograms
-// in LDS); the k candidates (all larger values, then the first equal ones in
+// order-preserving 32-bit key of each logit (3 passes over digits of 11, 11
+// and 10 bits, histograms in LDS); the k candidates (all larger values, then the first equal ones in
 // index order) are compacted into LDS, sorted by a bitonic network, and
 // scanned.  Whole-row draws scan per-thread contiguous segments.
 // Every reduction and scan has a fixed order: results do not vary between
@@ -33,6 +33,8 @@ namespace {
 
 constexpr int kSmpThreads = 1024;
 constexpr int kSmpWaves = kSmpThreads / kWave;
+constexpr int kSmpBins = 2048;   // radix-select histogram: 11-bit digits, two bins per thread
+static_assert(kSmpBins == 2 * kSmpThreads, "bin choice: each thread scans two adjacent bins");
 
 struct SampleParams {
   const float* logits;
@@ -258,27 +260,33 @@ __device__ void row_sample_topk(const SampleParams& p, const float* row, float u
   // ---- radix select: key of the k-th largest, and how many equal keys to take ----
   uint32_t prefix = 0, mask = 0;
   int remaining = k;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int b = threadIdx.x; b < 256; b += kSmpThreads) hist[b] = 0;
+  // three passes over digits of 11, 11 and 10 bits (2048 bins; the last pass uses the lower 1024)
+  for (int pass = 0; pass < 3; ++pass) {
+    const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+    const uint32_t dmask = pass == 2 ? 1023u : 2047u;
+    for (int b = threadIdx.x; b < kSmpBins; b += kSmpThreads) hist[b] = 0;
     __syncthreads();
     for_strided(row, vocab, [&](int, float v) __attribute__((always_inline)) {
       const uint32_t key = order_key(v);
-      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & dmask], 1u);
     });
     __syncthreads();
-    // the bin holding the remaining-th largest key: thread t < 256 takes bin 255 - t; an
-    // exclusive scan in that order gives the count of keys in higher bins
-    const int bin = 255 - static_cast<int>(threadIdx.x);
-    const int cnt = threadIdx.x < 256 ? static_cast<int>(hist[bin]) : 0;
+    // the bin holding the remaining-th largest key: thread t takes bins 2047 - 2t and 2046 - 2t,
+    // in that order; an exclusive scan over the pairs gives the count of keys in higher bins
+    const int hi_bin = kSmpBins - 1 - 2 * static_cast<int>(threadIdx.x);
+    const int c_hi = static_cast<int>(hist[hi_bin]), c_lo = static_cast<int>(hist[hi_bin - 1]);
     int all;
-    const int above = block_exclusive_scan<int>(cnt, reinterpret_cast<int*>(scan_tmp), all);
-    if (cnt > 0 && above < remaining && remaining <= above + cnt) {
-      misc[0] = bin;
+    const int above = block_exclusive_scan<int>(c_hi + c_lo, reinterpret_cast<int*>(scan_tmp), all);
+    if (c_hi > 0 && above < remaining && remaining <= above + c_hi) {
+      misc[0] = hi_bin;
       misc[1] = remaining - above;
+    } else if (c_lo > 0 && above + c_hi < remaining && remaining <= above + c_hi + c_lo) {
+      misc[0] = hi_bin - 1;
+      misc[1] = remaining - above - c_hi;
     }
     __syncthreads();
     prefix |= static_cast<uint32_t>(misc[0]) << shift;
-    mask |= 255u << shift;
+    mask |= dmask << shift;
     remaining = misc[1];
     __syncthreads();
   }
@@ -369,7 +377,7 @@ __device__ void row_sample_topk(const SampleParams& p, const float* row, float u
 
 __global__ __launch_bounds__(kSmpThreads) void sample_kernel(const SampleParams p) {
   __shared__ SmpShared sh;
-  __shared__ uint32_t hist[256];
+  __shared__ uint32_t hist[kSmpBins];
   __shared__ uint32_t ckey[kMaxTopK];
   __shared__ int cidx[kMaxTopK];
   __shared__ float scan_tmp[2 * kSmpWaves];
