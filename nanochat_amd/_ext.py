@@ -211,3 +211,37 @@ def read_and_clear_device_errors(device: torch.device) -> int:
     bits = int(flag.item())
     flag.zero_()
     return bits
+
+
+# What each device error bit means, in the words of the error the reference raises (or would
+# raise) for the same input.
+DEVICE_ERROR_MESSAGES = (
+    (NC_DEVERR_OVERFLOW, "cache_seqlens + T_new exceeds the cache length (the reference's slice "
+                         "assignment fails on the size mismatch)"),
+    (NC_DEVERR_ROPE_RANGE, "a position is beyond the rotary tables"),
+    (NC_DEVERR_BATCH_IDX, "cache_batch_idx holds an index outside the cache's batch dimension"),
+    (NC_DEVERR_QLEN, "cu_seqlens_q holds a row outside [0, total_q) or longer than max_seqlen_q"),
+    (NC_DEVERR_SAMPLE, "a row of logits has no finite value (torch.multinomial rejects such a row)"),
+    (NC_DEVERR_PAGE, "page_table holds a block index outside the cache"),
+)
+
+
+def raise_device_errors(bits: int, where: str) -> None:
+    """RuntimeError naming every NC_DEVERR_* bit set in `bits` (nothing if bits == 0)."""
+    if bits:
+        msgs = [m for b, m in DEVICE_ERROR_MESSAGES if bits & b] or [f"device error bits {bits:#x}"]
+        raise RuntimeError(f"{where}: " + "; ".join(msgs))
+
+
+def host_values_and_errors(t: torch.Tensor) -> tuple[list, int]:
+    """t's values on the host together with the device error flag, in ONE device-to-host copy.
+
+    For host synchronisations the caller makes anyway (KVCache.get_pos, the engine's sampled
+    ids): the flag rides along, so surfacing kernel errors adds no synchronisation.  A set flag
+    is cleared (on the current stream) and its bits returned."""
+    flag = error_flag(t.device)
+    vals = torch.cat((t.reshape(-1).to(torch.int64), flag.to(torch.int64))).tolist()
+    bits = int(vals[-1])
+    if bits:
+        flag.zero_()
+    return vals[:-1], bits

@@ -231,12 +231,20 @@ __device__ void row_sample_full(const SampleParams& p, const float* row, float u
   const float target = u * total;
   if (threadIdx.x == 0) { pick[0] = INT32_MAX; pick[1] = -1; }
   __syncthreads();
-  if (local > 0.0f && excl <= target && target < excl + local) {
+  // The segments' fp32 intervals [excl, excl + local) need not tile exactly
+  // (excl of thread t + 1 can differ from excl + local of thread t by a
+  // rounding), so there is no lower bound: every segment whose upper end lies
+  // above the target looks for its first drawable element whose running sum
+  // passes the target (its last drawable one if rounding leaves none), and
+  // the lowest index wins.  A target in a rounding gap between two segments
+  // then draws the first drawable element after the gap.
+  if (local > 0.0f && target < excl + local) {
     float run = excl;
-    int chosen = last_pos;   // rounding: the crossing is in this segment
+    int chosen = last_pos;
     for (int i = i0; i < i1; ++i) {
-      run += expf(finite_or_neg_inf(row[i]) * p.inv_temp - rmax);
-      if (run > target) { chosen = i; break; }
+      const float e = expf(finite_or_neg_inf(row[i]) * p.inv_temp - rmax);
+      run += e;
+      if (e > 0.0f && run > target) { chosen = i; break; }
     }
     atomicMin(pick, chosen);
   }

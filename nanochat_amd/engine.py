@@ -52,7 +52,16 @@ class KVCache:
         self.prev_embedding = None
 
     def get_pos(self):
-        """Row 0's position (uniform-batch assumption of nanochat/engine.py:111-113)."""
+        """Row 0's position (uniform-batch assumption of nanochat/engine.py:111-113).
+
+        On the GPU this host read also carries the kernels' device error flag (the same single
+        copy), and a set flag raises RuntimeError here: e.g. an append past the cache length,
+        which the reference's slice assignment rejects at the call (flash_attention.py:160-162).
+        """
+        if self.cache_seqlens.is_cuda:
+            vals, bits = _ext.host_values_and_errors(self.cache_seqlens[:1])
+            _ext.raise_device_errors(bits, "KV-cache path")
+            return vals[0]
         return self.cache_seqlens[0].item()
 
     def get_layer_cache(self, layer_idx):
@@ -223,15 +232,21 @@ class GraphDecodeStep:
 class Engine:
     """Batched generation with one prefill and a fanned-out KV cache."""
 
-    def __init__(self, model, tokenizer, use_graph=None, fused_sampling=None):
+    def __init__(self, model, tokenizer, use_graph=None, fused_sampling=None, cache_dtype=None):
         self.model = model
         self.tokenizer = tokenizer
         # None: replay decode steps from a HIP graph whenever the model runs the fused QK prologue on the GPU
         self.use_graph = use_graph
-        # None: sample with the HIP kernel (nc_sample) on the GPU (top_k up to 1024).  Same
-        # distribution as the reference's torch.multinomial, one torch.rand draw per row from the
-        # same generator; greedy decoding gives the same tokens either way.  False keeps the torch ops.
+        # Sampling on the GPU.  None (default): greedy steps (temperature 0) run the HIP kernel
+        # (nc_sample's argmax is bit-identical to torch.argmax) and draws at temperature > 0 run
+        # the reference's torch ops, so a seeded run draws the reference's torch.multinomial
+        # stream.  True: draws run the kernel too (top_k up to 1024): the same distribution, one
+        # torch.rand uniform per row from the same generator, hence a different stream of
+        # tokens for a given seed.  False: torch's ops for every step.
         self.fused_sampling = fused_sampling
+        # KV-cache dtype; None applies the reference's rule (bf16 on a GPU, fp32 elsewhere,
+        # nanochat/engine.py:186).  Tests set float32 to compare with fp32 golden runs.
+        self.cache_dtype = cache_dtype
 
     def _graph_decode(self, device):
         if device.type != "cuda" or not getattr(self.model, "fused_qk_prologue", False):
@@ -244,6 +259,8 @@ class Engine:
         assert isinstance(tokens, list) and isinstance(tokens[0], int), "expecting list of ints"
         device = self.model.get_device()
         dtype = torch.bfloat16 if device.type == "cuda" else torch.float32
+        if self.cache_dtype is not None:
+            dtype = self.cache_dtype
         rng = torch.Generator(device=device)
         rng.manual_seed(seed)
         special = self.tokenizer.encode_special
@@ -265,8 +282,11 @@ class Engine:
         del prefill_cache
 
         step = GraphDecodeStep(self.model, cache, num_samples, device) if self._graph_decode(device) else None
-        fused = (device.type == "cuda" and self.fused_sampling is not False
-                 and (top_k is None or top_k <= gpu_sampling.MAX_TOP_K))   # larger top_k: torch's ops
+        if temperature == 0.0:
+            fused = device.type == "cuda" and self.fused_sampling is not False
+        else:   # draws: the kernel only on request, and for top_k it supports
+            fused = (device.type == "cuda" and self.fused_sampling is True
+                     and (top_k is None or top_k <= gpu_sampling.MAX_TOP_K))
         sampler = gpu_sampling.sample_next_token if fused else sample_next_token
         rows = [RowState(tokens.copy()) for _ in range(num_samples)]
         generated = 0
@@ -275,7 +295,13 @@ class Engine:
                 break
             if all(r.completed for r in rows):
                 break
-            sampled = sampler(logits, rng, temperature, top_k)[:, 0].tolist()
+            next_ids = sampler(logits, rng, temperature, top_k)[:, 0]
+            if next_ids.is_cuda:
+                # the per-step host read of the ids also carries the kernels' error flag
+                sampled, bits = _ext.host_values_and_errors(next_ids)
+                _ext.raise_device_errors(bits, "Engine.generate")
+            else:
+                sampled = next_ids.tolist()
             column, masks = [], []
             for i, r in enumerate(rows):
                 forced = len(r.forced_tokens) > 0

@@ -190,18 +190,12 @@ def _attach_workspace(a, dev, stream, need):
 
 
 def _check_device_errors(name, dev):
+    """NANOCHAT_AMD_CHECK=1: read the device error flag after every call (one host sync each).
+
+    By default the flag is read, and raised as RuntimeError, at the host synchronisations the
+    callers already make: KVCache.get_pos and the engine's per-step sampled ids."""
     if _CHECK_ERRORS:
-        bits = _ext.read_and_clear_device_errors(dev)
-        if bits & _ext.NC_DEVERR_OVERFLOW:
-            raise RuntimeError(f"{name}: cache_seqlens + T_new exceeds the cache length")
-        if bits & _ext.NC_DEVERR_ROPE_RANGE:
-            raise RuntimeError(f"{name}: a position is beyond the rotary tables")
-        if bits & _ext.NC_DEVERR_BATCH_IDX:
-            raise RuntimeError(f"{name}: cache_batch_idx holds an index outside the cache's batch dimension")
-        if bits & _ext.NC_DEVERR_QLEN:
-            raise RuntimeError(f"{name}: cu_seqlens_q holds a row outside [0, total_q) or longer than max_seqlen_q")
-        if bits & _ext.NC_DEVERR_PAGE:
-            raise RuntimeError(f"{name}: page_table holds a block index outside the cache")
+        _ext.raise_device_errors(_ext.read_and_clear_device_errors(dev), name)
 
 
 def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,

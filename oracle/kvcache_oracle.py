@@ -210,12 +210,6 @@ class KVCache:
             self.prev_embedding = other.prev_embedding.expand(self.batch_size, -1, -1).clone()
 
 
-def kv_fanout(dst_k, dst_v, src_k, src_v, prefix_len):
-    """The broadcast copy of nanochat/engine.py:132-133 on (L, B, T, H, D) slabs."""
-    dst_k[:, :, :prefix_len, :, :] = src_k[:, :, :prefix_len, :, :]
-    dst_v[:, :, :prefix_len, :, :] = src_v[:, :, :prefix_len, :, :]
-
-
 def compute_window_sizes(sequence_len, window_pattern, n_layer):
     """nanochat/gpt.py:285-312: per-layer (left, right) windows, last layer long."""
     pattern = window_pattern.upper()

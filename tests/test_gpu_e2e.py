@@ -7,7 +7,10 @@
   smallest top-1/top-2 logit gap along the golden runs is 3.4e-5 (init) and
   2.2e-4 (perturbed), far above fp32 GPU/CPU GEMM differences.
 - Engine.generate on the GPU (bf16 cache by nanochat's dtype rule) equals a
-  hand-driven loop over the same KVCache and model.
+  hand-driven loop over the same KVCache and model; with an fp32 cache it
+  reproduces the golden tokens itself (init and perturbed weights).
+- Draws at temperature > 0 follow the reference's torch.multinomial stream by
+  default; kernel errors raise at the engine's per-step host read.
 - nanochat's Engine tests (tests/test_engine.py:158-267) re-expressed with
   the mock model on the GPU (they exercise the fan-out prefill).
 - C3-shaped Engine.generate (d24, 1024-token prompt, 16 samples, 128 steps).
@@ -16,6 +19,7 @@ import pytest
 import torch
 
 import nanochat_amd.gpt as gpt
+from nanochat_amd import _ext
 from nanochat_amd.engine import Engine, KVCache
 from tests.test_model_cpu import GOLDEN, SpecialTokens, c1_model
 
@@ -201,6 +205,14 @@ def test_c3_engine_generate_d24():
         assert len(column) == 16 and all(0 <= t < 32768 for t in column)
         steps += 1
     assert steps == 128
+    # greedy: the fan-out gives 16 copies of one prefilled row, and every kernel on the path treats
+    # rows independently, so the 16 greedy continuations must stay identical token for token
+    cols = [col for col, _ in engine.generate(prompt, num_samples=16, max_tokens=32, temperature=0.0)]
+    assert len(cols) == 32 and all(len(set(col)) == 1 for col in cols)
+    # and a seeded run is reproducible
+    a = [col for col, _ in engine.generate(prompt, num_samples=16, max_tokens=8, temperature=1.0, seed=3)]
+    b = [col for col, _ in engine.generate(prompt, num_samples=16, max_tokens=8, temperature=1.0, seed=3)]
+    assert a == b
 
 
 # ---- the fused QK prologue in the model (rotary/norm/x1.2 inside the cache call) ----
@@ -349,3 +361,62 @@ def test_small_m_projections_in_the_model(monkeypatch):
         assert float((a - b).abs().max()) <= 2e-2 * float(b.abs().max()) + 1e-3
     assert torch.equal(outs[0][1].cache_seqlens, outs[1][1].cache_seqlens)
     assert float((outs[0][1].k_cache.float() - outs[1][1].k_cache.float()).abs().max()) <= 0.05
+
+
+# ---- Engine.generate against the reference's golden tokens and sampling stream ----
+@pytest.mark.parametrize("variant", ["init", "perturbed"])
+def test_c1_engine_generate_matches_reference_tokens_fp32_cache(variant):
+    """Engine.generate itself (prefill, fan-out, graph-replayed decode, fused prologue, greedy steps on
+    the sampling kernel) on the GPU with an fp32 cache reproduces the reference's 64 golden tokens.
+    The perturbed weights make attention and the smear state change the logits."""
+    model = c1_model(variant).to(DEV)
+    engine = Engine(model, SpecialTokens(), cache_dtype=torch.float32)
+    out = [col[0] for col, _ in engine.generate(GOLDEN["prompt"], num_samples=1, max_tokens=64, temperature=0.0)]
+    assert out == GOLDEN[variant]["tokens"]
+
+
+def test_engine_default_draws_are_the_reference_torch_multinomial_stream():
+    """At temperature > 0 the default engine draws with the reference's own ops (topk, softmax,
+    torch.multinomial on the seeded generator, nanochat/engine.py:141-156), so a seed gives the
+    reference's tokens; fused_sampling=True opts into the kernel's draws (same distribution, one
+    uniform per row, hence another stream)."""
+    model = c1_model("perturbed").to(DEV)
+    runs = {}
+    for fused in (None, False, True):
+        engine = Engine(model, SpecialTokens(), fused_sampling=fused)
+        runs[fused] = [col for col, _ in engine.generate(GOLDEN["prompt"], num_samples=4, max_tokens=12,
+                                                         temperature=0.9, top_k=50, seed=11)]
+    assert runs[None] == runs[False]
+    assert all(0 <= t < 32768 for col in runs[True] for t in col)
+
+
+def test_engine_raises_device_errors_at_its_per_step_read():
+    """A kernel error flagged during a decode step (here an append past a full cache, which the
+    reference rejects at the call) raises RuntimeError at the engine's per-step host read of the
+    sampled ids, which carries the flag with no extra synchronisation."""
+    from nanochat_amd.flash_attention import flash_attn
+
+    class OverflowingModel(MockModel):
+        def __init__(self):
+            super().__init__()
+            self.calls = 0
+            self.full = KVCache(batch_size=1, num_heads=1, seq_len=4, head_dim=64, num_layers=1, device=DEV,
+                                dtype=torch.bfloat16)
+            self.full.cache_seqlens.fill_(4)
+
+        def forward(self, ids, kv_cache=None):
+            self.calls += 1
+            if self.calls == 3:   # the second decode step appends into a full cache
+                x = torch.ones(1, 1, 1, 64, dtype=torch.bfloat16, device=DEV)
+                kc, vc = self.full.get_layer_cache(0)
+                flash_attn.flash_attn_with_kvcache(x, kc, vc, k=x, v=x, cache_seqlens=self.full.cache_seqlens)
+            return super().forward(ids, kv_cache)
+
+    _ext.read_and_clear_device_errors(DEV)
+    engine = Engine(OverflowingModel(), ByteTokenizer())
+    steps = 0
+    with pytest.raises(RuntimeError, match="exceeds the cache length"):
+        for _ in engine.generate(PROMPT, max_tokens=8, temperature=0.0):
+            steps += 1
+    assert steps == 2
+    assert _ext.read_and_clear_device_errors(DEV) == 0

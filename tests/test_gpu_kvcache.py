@@ -158,3 +158,53 @@ def test_d24_fanout_full_size():
         assert torch.equal(dst.v_cache[:, n, :P], src.v_cache[:, 0])
     assert (dst.k_cache[:, :, P:] == 0).all() and (dst.v_cache[:, :, P:] == 0).all()
     assert (dst.cache_seqlens == P).all()
+
+
+def test_reset_on_gpu_zeroes_positions_and_keeps_cache_bytes():
+    """KVCache.reset (nanochat/engine.py:106-109) on the GPU: positions back to 0, prev_embedding
+    dropped, cache bytes kept; the next append then writes at position 0 again (mirrors
+    nanochat tests/test_engine.py:114-116)."""
+    from nanochat_amd.flash_attention import flash_attn
+    B, T_max, H, D = 3, 32, 2, 64
+    cache = KVCache(batch_size=B, num_heads=H, seq_len=T_max, head_dim=D, num_layers=2, device=DEV,
+                    dtype=torch.bfloat16)
+    g = gen(401)
+    for layer in range(2):
+        kc, vc = cache.get_layer_cache(layer)
+        q, k, v = (randn((B, 5, H, D), g, torch.bfloat16).to(DEV) for _ in range(3))
+        flash_attn.flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=cache.cache_seqlens, causal=True)
+    cache.advance(5)
+    cache.prev_embedding = torch.ones(B, 1, 8, device=DEV)
+    assert cache.get_pos() == 5
+    k_before, v_before = cache.k_cache.clone(), cache.v_cache.clone()
+    cache.reset()
+    assert cache.get_pos() == 0 and cache.cache_seqlens.tolist() == [0] * B
+    assert cache.prev_embedding is None
+    assert torch.equal(bits(cache.k_cache), bits(k_before)) and torch.equal(bits(cache.v_cache), bits(v_before))
+    kc, vc = cache.get_layer_cache(0)
+    k1 = randn((B, 1, H, D), g, torch.bfloat16).to(DEV)
+    flash_attn.flash_attn_with_kvcache(k1, kc, vc, k=k1, v=k1, cache_seqlens=cache.cache_seqlens)
+    want = k_before.clone()
+    want[0, :, 0] = k1[:, 0]
+    assert torch.equal(bits(cache.k_cache), bits(want)), "after reset the append lands at position 0"
+
+
+def test_overflow_raises_at_get_pos():
+    """An append past the cache length raises RuntimeError at the next host read of the positions
+    (KVCache.get_pos, which GPT.forward and prefill make anyway), as the reference's slice
+    assignment raises at the call (nanochat/flash_attention.py:160-162); the flag is then clear."""
+    from nanochat_amd.flash_attention import flash_attn
+    dev = torch.device(DEV, torch.cuda.current_device())
+    _ext.read_and_clear_device_errors(dev)
+    B, T_max, H, D = 2, 8, 2, 64
+    cache = KVCache(batch_size=B, num_heads=H, seq_len=T_max, head_dim=D, num_layers=1, device=DEV,
+                    dtype=torch.bfloat16)
+    cache.advance(T_max)                              # full
+    kc, vc = cache.get_layer_cache(0)
+    x = torch.ones(B, 1, H, D, dtype=torch.bfloat16, device=DEV)
+    before = cache.k_cache.clone()
+    flash_attn.flash_attn_with_kvcache(x, kc, vc, k=x, v=x, cache_seqlens=cache.cache_seqlens)
+    with pytest.raises(RuntimeError, match="exceeds the cache length"):
+        cache.get_pos()
+    assert cache.get_pos() == T_max                   # cleared: the next read is clean
+    assert torch.equal(bits(cache.k_cache), bits(before)), "nothing stored past the end"

@@ -37,6 +37,8 @@ def _int_operands(seed, m, n, k, dtype):
     (32, 3840, 1280), (9, 2100, 520), (32, 136, 4104), (2, 24, 392),
     # narrow plan with two column tiles per wave (m > 16, wide n), ragged last block
     (20, 4100, 264), (32, 6144, 1536),
+    # two column tiles per wave AND K split over two workgroups (ticket merge of the 2-tile partials)
+    (32, 5120, 2048), (24, 6144, 2304),
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_linear_exact_on_integer_operands(m, n, k, dtype):
@@ -46,6 +48,17 @@ def test_linear_exact_on_integer_operands(m, n, k, dtype):
     got = linear(x.to(DEV), w.to(DEV)).cpu()
     assert got.dtype == dtype and got.shape == (m, n)
     assert torch.equal(bits(got), bits(want)), (m, n, k, dtype)
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 5120, 2048), (24, 6144, 2304)])
+def test_two_tile_split_plan_is_the_one_exercised(m, n, k):
+    """The shapes above reach the narrow kernel with two 16-column tiles per wave and K split over
+    two workgroups: the workspace holds exactly that plan's partials (64 KiB of split counters,
+    then blocks x splits x tiles x row tiles x 64 lanes x 4 fp32 values)."""
+    lib = _ext.lib()
+    blocks, splits, tiles, row_tiles = (n + 31) // 32, 2, 2, (m + 15) // 16
+    want = _ext.NC_WORKSPACE_SYNC_BYTES + blocks * splits * tiles * row_tiles * 64 * 4 * 4
+    assert lib.nc_linear_workspace_bytes(m, n, k) == want
 
 
 @pytest.mark.parametrize("m,n,k", [(32, 1280, 1280), (32, 1280, 5120), (7, 333, 1000), (64, 2048, 512)])

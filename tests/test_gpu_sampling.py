@@ -83,6 +83,28 @@ def test_whole_row_draws_match_oracle(V, T):
     _compare_draws(x, u, T, None)
 
 
+def test_whole_row_draw_at_segment_boundaries():
+    """u planted at the boundaries of the kernel's 1024 per-thread segments (32 logits each at
+    V = 32768), and one float32 ulp either side: the fp32 segment sums need not tile [0, total)
+    exactly, and a target between two segments must still draw a category next to the boundary
+    (the last of segment t or the first of segment t + 1), never a far one.  Logits are flat
+    enough (N(0, 0.3^2)) that each of those two categories is wider than the fp32 rounding."""
+    V, seg = 32768, 32
+    row = _logits(12, 1, V, scale=0.3)[0]
+    p = torch.softmax(row.double(), 0)
+    cum = torch.cumsum(p.view(-1, seg).sum(1), 0)[:-1]        # mass through segment t, t < 1023
+    us, seg_of = [], []
+    for t, c in enumerate(cum.tolist()):
+        for f in (1 - 2 ** -23, 1.0, 1 + 2 ** -23):
+            us.append(min(c * f, 1 - 2 ** -24))
+            seg_of.append(t)
+    u = torch.tensor(us, dtype=torch.float32)
+    x = row.to(DEV).expand(len(us), -1)                       # one row, stride 0
+    got = sample_with_uniforms(x, u.to(DEV), 1.0, None).cpu()[:, 0]
+    for i, t in enumerate(seg_of):
+        assert int(got[i]) in (seg * t + seg - 1, seg * (t + 1)), (t, us[i], int(got[i]))
+
+
 @pytest.mark.parametrize("V,k,T", [(32768, 1, 1.0), (32768, 5, 1.0), (32768, 50, 0.7), (32768, 200, 1.0),
                                    (32768, 1024, 1.3), (1000, 999, 1.0), (300, 64, 0.9), (50257, 50, 1.0),
                                    (65536, 1024, 0.8)])
