@@ -49,8 +49,11 @@ constexpr int64_t kWideMaxKeys = 4096;
 #ifndef NC_DECODE_MERGE_IN_KERNEL
 #define NC_DECODE_MERGE_IN_KERNEL 1  // 0: decode splits always use the merge launch
 #endif
+#ifndef NC_MERGE_IN_KERNEL_MAX_WG
+#define NC_MERGE_IN_KERNEL_MAX_WG 2048
+#endif
 constexpr int64_t kMaxTickets = NC_WORKSPACE_SYNC_BYTES / 4;
-constexpr int64_t kMergeInKernelMaxWG = NC_DECODE_MERGE_IN_KERNEL ? 2048 : 0;
+constexpr int64_t kMergeInKernelMaxWG = NC_DECODE_MERGE_IN_KERNEL ? NC_MERGE_IN_KERNEL_MAX_WG : 0;
 
 bool valid_dtype(int d) { return d == NC_DTYPE_F32 || d == NC_DTYPE_F16 || d == NC_DTYPE_BF16; }
 int64_t dtype_bytes(int d) { return d == NC_DTYPE_F32 ? 4 : 2; }
