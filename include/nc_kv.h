@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define NC_KV_ABI_VERSION 7
+#define NC_KV_ABI_VERSION 8
 
 /* Element types (the torch dtypes the reference path uses). */
 enum nc_dtype {
@@ -44,7 +44,9 @@ enum nc_status {
   NC_ERR_HEAD_DIM = 4,          /* head_dim not in the compiled set         */
   NC_ERR_ALIGNMENT = 5,         /* pointer / stride not 16-byte aligned     */
   NC_ERR_WORKSPACE = 6,         /* workspace NULL or smaller than required  */
-  NC_ERR_LAUNCH = 7             /* hipLaunchKernel / hipGetLastError failed */
+  NC_ERR_LAUNCH = 7,            /* hipLaunchKernel / hipGetLastError failed */
+  NC_ERR_SCRATCH_LIMIT = 8      /* nc_attn_kvcache_noalloc: the call needs more than
+                                   NC_NOALLOC_SCRATCH_BYTES of scratch */
 };
 
 /* Bit set in *error_flag by a kernel when a row would write past t_max
@@ -203,6 +205,26 @@ typedef struct nc_attn_args {
 size_t nc_attn_workspace_bytes(const nc_attn_args* args);
 
 int nc_attn_kvcache(const nc_attn_args* args, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * nc_attn_kvcache_noalloc: no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The same call as nc_attn_kvcache
+ * (same kernels, plans and results), except that its split-K scratch (split
+ * counters and partials) lives in a device array of the library, of
+ * NC_NOALLOC_SCRATCH_BYTES on each GPU it runs on, held until the process
+ * ends; args->workspace and args->workspace_bytes are ignored.  It calls no
+ * hipMalloc / hipFree.  A call needing more scratch than that
+ * (nc_attn_workspace_bytes(args) > NC_NOALLOC_SCRATCH_BYTES) returns
+ * NC_ERR_SCRATCH_LIMIT and launches nothing.  Every call on one GPU shares
+ * that GPU's array: calls that overlap in time on one GPU (other streams,
+ * other host threads) race and must be serialised by the caller.  The first
+ * call on a GPU looks the array up and launches one small kernel on `stream`
+ * that zeroes its split counters; every call leaves them zero.
+ * ------------------------------------------------------------------------- */
+#define NC_NOALLOC_SCRATCH_BYTES (64 << 20)
+
+int nc_attn_kvcache_noalloc(const nc_attn_args* args, void* stream);
 
 /* ---------------------------------------------------------------------------
  * QK prologue fused into the call: nanochat/gpt.py:98-102 (rotary, QK RMS

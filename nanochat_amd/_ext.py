@@ -16,7 +16,7 @@ import torch
 # NANOCHAT_AMD_LIB points at another build of the same library (e.g. a tuning
 # variant); by default the in-tree build next to this file is loaded.
 LIB_PATH = Path(os.environ.get("NANOCHAT_AMD_LIB", Path(__file__).resolve().parent / "libnc_kv.so"))
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -28,6 +28,9 @@ NC_DEVERR_SAMPLE = 16
 NC_DEVERR_PAGE = 32
 # leading workspace bytes holding split counters: zero before first use, left zero by every call
 NC_WORKSPACE_SYNC_BYTES = 65536
+# device scratch nc_attn_kvcache_noalloc holds on each GPU (its largest call's workspace)
+NC_NOALLOC_SCRATCH_BYTES = 64 << 20
+NC_ERR_SCRATCH_LIMIT = 8
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -120,6 +123,7 @@ EXPORTS = {
     "nc_kv_fanout": (ctypes.c_int, [ctypes.POINTER(FanoutArgs), _c_void_p]),
     "nc_attn_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
     "nc_attn_kvcache": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _c_void_p]),
+    "nc_attn_kvcache_noalloc": (ctypes.c_int, [ctypes.POINTER(AttnArgs), _c_void_p]),
     "nc_attn_rope_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
     "nc_attn_kvcache_rope": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.POINTER(QKPrologue), _c_void_p]),
     "nc_linear_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64]),

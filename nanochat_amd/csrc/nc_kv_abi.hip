@@ -1,9 +1,12 @@
 // C ABI entry points of libnc_kv.so: argument validation, launch planning and
-// dispatch.  Nothing here allocates, synchronises or keeps mutable state.
+// dispatch.  Nothing here allocates or synchronises.  The only mutable state is
+// the per-device address of the no-allocation entry point's scratch array
+// (set once per device, under a mutex).
 
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "nc_kv.h"
 #include "nc_kv_internal.hpp"
@@ -220,6 +223,9 @@ const char* nc_strerror(int status) {
     case NC_ERR_ALIGNMENT: return "pointer or stride not 16-byte aligned";
     case NC_ERR_WORKSPACE: return "workspace missing or too small";
     case NC_ERR_LAUNCH: return "kernel launch failed";
+    case NC_ERR_SCRATCH_LIMIT:
+      return "the call needs more split-K scratch than nc_attn_kvcache_noalloc holds (NC_NOALLOC_SCRATCH_BYTES); "
+             "use nc_attn_kvcache with a workspace";
     default: return "unknown nc_status";
   }
 }
@@ -397,6 +403,82 @@ int nc_attn_kvcache(const nc_attn_args* args, void* stream) {
     return NC_ERR_WORKSPACE;
   }
   return run_attention(a, plan, carve(a, plan), nullptr, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Scratch of nc_attn_kvcache_noalloc: the split counters (first
+// NC_WORKSPACE_SYNC_BYTES, zero between calls) and split partials that
+// nc_attn_kvcache takes from the caller's workspace.  Each GPU holds its own
+// copy at its own address until the process ends.  In host code this name is
+// not a device address: host code only ever uses the address
+// hipGetSymbolAddress returns for a device (kept in g_scratch_addr).
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[NC_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 1024;
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kMaxScratchDevices];  // device address of `scratch` per device; null until set up
+
+__global__ __launch_bounds__(256) void clear_counters_kernel(uint32_t* counters) {
+  counters[blockIdx.x * 256 + threadIdx.x] = 0u;
+}
+
+// Device address of `scratch` on the GPU that `stream` belongs to.  The first
+// call on a device looks the address up with that device current and clears
+// the split counters with a fill kernel on `stream`, ordered before the
+// call's own kernels (static device memory is zero at load, but the counters
+// must be zero whatever the loader did).
+int scratch_address(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (stream != nullptr ? hipStreamGetDevice(stream, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) {
+    return NC_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) return NC_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_addr[dev] == nullptr) {
+    int prev = -1;
+    if (hipGetDevice(&prev) != hipSuccess) return NC_ERR_LAUNCH;
+    if (prev != dev && hipSetDevice(dev) != hipSuccess) return NC_ERR_LAUNCH;
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p != nullptr) {
+      static_assert(NC_WORKSPACE_SYNC_BYTES % (4 * 256) == 0, "counter region: whole 256-thread blocks");
+      hipLaunchKernelGGL(clear_counters_kernel, dim3(NC_WORKSPACE_SYNC_BYTES / (4 * 256)), dim3(256), 0, stream,
+                         static_cast<uint32_t*>(p));
+      e = hipGetLastError();
+    }
+    if (prev != dev) (void)hipSetDevice(prev);
+    if (e != hipSuccess || p == nullptr) return NC_ERR_LAUNCH;
+    g_scratch_addr[dev] = p;
+  }
+  *out = g_scratch_addr[dev];
+  return NC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nc_attn_kvcache_noalloc(const nc_attn_args* args, void* stream) {
+  if (args == nullptr) return NC_ERR_NULL_ARG;
+  AttnPlan plan;
+  const int st = check_attention(*args, &plan);
+  if (st != NC_OK) return st;
+  if (plan.total_bytes > static_cast<size_t>(NC_NOALLOC_SCRATCH_BYTES)) return NC_ERR_SCRATCH_LIMIT;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  nc_attn_args a = *args;
+  a.workspace = nullptr;
+  a.workspace_bytes = 0;
+  if (plan.total_bytes > 0) {
+    const int s2 = scratch_address(hs, &a.workspace);
+    if (s2 != NC_OK) return s2;
+    a.workspace_bytes = NC_NOALLOC_SCRATCH_BYTES;
+  }
+  return run_attention(a, plan, carve(a, plan), nullptr, hs);
 }
 
 size_t nc_attn_rope_workspace_bytes(const nc_attn_args* args) {

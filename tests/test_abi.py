@@ -57,7 +57,7 @@ def test_struct_layouts_match_header_field_order():
 
 def test_strerror_names_every_status():
     lib = _ext.lib()
-    for code in range(8):
+    for code in range(9):
         assert lib.nc_strerror(code).decode()
     assert lib.nc_strerror(0).decode() == "ok"
     assert lib.nc_strerror(99).decode() == "unknown nc_status"
