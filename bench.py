@@ -20,9 +20,11 @@ PyTorch fallback) timed on this host's cores on a bounded sample.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import re
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -32,6 +34,8 @@ import torch
 ROOT = Path(__file__).resolve().parent
 METRIC = "decode attn+KV-append HBM GB/s (% of peak) and decode tokens/sec, d20 B=32"
 HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+REPLAYS = 21   # timed graph replays per figure; the median is reported
 
 # C2 shapes
 LAYERS, BATCH, HEADS, KV_HEADS, HEAD_DIM = 20, 32, 10, 10, 128
@@ -78,7 +82,7 @@ def read_traffic():
 
 
 def copy_ceiling(dev, stream, nbytes=1 << 31, reps=10) -> float:
-    """Achievable streaming bandwidth on this GPU: torch's device copy of 2 GiB, read + write bytes."""
+    """torch's device copy of 2 GiB, read + write bytes (a copy ceiling; the decode kernel mostly reads)."""
     with torch.cuda.stream(stream):
         src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).fill_(1.0)
         dst = torch.empty_like(src)
@@ -95,12 +99,94 @@ def copy_ceiling(dev, stream, nbytes=1 << 31, reps=10) -> float:
     return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
+def _probe_lib():
+    """nanochat_amd/libnc_probe.so: bench.py's read-bandwidth probes (built with the library)."""
+    path = ROOT / "nanochat_amd" / "libnc_probe.so"
+    lib = ctypes.CDLL(str(path))
+    lib.nc_probe_read_linear.restype = ctypes.c_int
+    lib.nc_probe_read_linear.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    lib.nc_probe_read_kv_rows.restype = ctypes.c_int
+    lib.nc_probe_read_kv_rows.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                          ctypes.c_void_p, ctypes.c_void_p]
+    return lib
+
+
+def _event_ms(stream, fn, reps):
+    """Median ms of `reps` calls of fn(), each bracketed by HIP events on `stream` (after one warm call)."""
+    with torch.cuda.stream(stream):
+        fn()
+        evs = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            evs.append((e0, e1))
+        stream.synchronize()
+    return statistics.median(e0.elapsed_time(e1) for e0, e1 in evs)
+
+
+def read_ceilings(dev, stream, k_cache, v_cache, seqlens, c2_call_bytes) -> dict:
+    """Read-bandwidth ceilings measured on this GPU by libnc_probe.so (read-only kernels):
+    - read_linear: one non-temporal pass over a 4 GiB buffer, 32 KiB contiguous per workgroup (the HBM
+      streaming read rate);
+    - read_c2_shape: the K/V bytes of one C2 decode call (layer 0 of the bench's caches, positions
+      [0, s_b] of every row and head) in the decode kernel's access shape (256-byte head rows at the
+      2560-byte token stride, 256-position workgroups), with no arithmetic and no output."""
+    lib = _probe_lib()
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    nbytes = 1 << 32
+    with torch.cuda.stream(stream):
+        buf = torch.ones(nbytes // 2, dtype=torch.bfloat16, device=dev)
+    sh = stream.cuda_stream
+
+    def lin():
+        assert lib.nc_probe_read_linear(buf.data_ptr(), nbytes, sink.data_ptr(), sh) == 0
+
+    ms_lin = _event_ms(stream, lin, 10)
+    del buf
+    B, T, Hkv, D = k_cache.shape
+
+    def rows():
+        assert lib.nc_probe_read_kv_rows(k_cache.data_ptr(), v_cache.data_ptr(), seqlens.data_ptr(), B, Hkv, T,
+                                         k_cache.stride(0), k_cache.stride(1), 256, sink.data_ptr(), sh) == 0
+
+    ms_rows = _event_ms(stream, rows, REPLAYS)
+    kv_bytes = sum(2 * Hkv * D * 2 * (int(s) + 1) for s in seqlens.tolist())
+    return {"read_linear_GBps": round(nbytes / (ms_lin * 1e-3) / 1e9, 1),
+            "read_c2_shape_GBps": round(kv_bytes / (ms_rows * 1e-3) / 1e9, 1),
+            "read_c2_shape_us": round(ms_rows * 1e3, 2),
+            "read_c2_shape_kv_bytes": kv_bytes,
+            "note": "libnc_probe.so read-only kernels: read_linear = one non-temporal pass over 4 GiB; "
+                    "read_c2_shape = one C2 call's K/V bytes in the decode kernel's access shape, no compute"}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cgroup_cpus():
+    """CPU quota of this process's cgroup in cores (cgroup v2 cpu.max), or None if unlimited/unknown."""
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        return None if quota == "max" else round(int(quota) / int(period), 2)
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_baseline(budget_s: float) -> dict:
-    """Time the oracle (reference fallback restated, row by row) on the host cores."""
+    """Time the oracle (reference fallback restated, row by row) on all the host cores this process may use."""
     sys.path.insert(0, str(ROOT))
     from oracle import kvcache_oracle as orc
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     g = torch.Generator(device="cpu")
     g.manual_seed(0)
@@ -127,16 +213,31 @@ def cpu_baseline(budget_s: float) -> dict:
         "cores": cores,
         "kind": "port",
         "sample": f"{layer_steps} layer-steps of C2 decode (2 of 20 layers, B=32, bf16) in {dt:.1f} s "
-                  f"through oracle/kvcache_oracle.py (torch CPU SDPA, row by row)",
+                  f"through oracle/kvcache_oracle.py (torch CPU SDPA, row by row), "
+                  f"torch.set_num_threads({cores}) = len(os.sched_getaffinity(0))",
+        "cpu_model": _cpu_model(),
+        "cgroup_cpu_quota_cores": _cgroup_cpus(),
     }
 
 
-# ---------------------------------------------------------------------------
-# Further BASELINE.json configs (python bench.py --config c3|c4|c5): one JSON
-# line each with per-phase figures.  The default run (c2) is the metric line.
-# ---------------------------------------------------------------------------
-def _graph_time(stream, body, reset, reps=1):
-    """Capture body() in a HIP graph (after one eager run), time `reps` replays with HIP events."""
+def _replay_times(stream, graph, reset, reps):
+    """Per-replay times (ms) of `reps` replays of `graph`: reset() runs before each replay, outside
+    the HIP events on `stream` that bracket the replay itself."""
+    evs = []
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            reset()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            graph.replay()
+            e1.record(stream)
+            evs.append((e0, e1))
+        stream.synchronize()
+    return [e0.elapsed_time(e1) for e0, e1 in evs]
+
+
+def _graph_time(stream, body, reset, reps=REPLAYS):
+    """Capture body() in a HIP graph (after one eager run); median ms of `reps` timed replays."""
     with torch.cuda.stream(stream):
         body()
         reset()
@@ -147,15 +248,10 @@ def _graph_time(stream, body, reset, reps=1):
     with torch.cuda.stream(stream):
         reset()
         graph.replay()
-        reset()
         stream.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        e1.record(stream)
-        stream.synchronize()
-    return e0.elapsed_time(e1) / reps
+    ms = statistics.median(_replay_times(stream, graph, reset, reps))
+    del graph
+    return ms
 
 
 def _kv_bytes(seqlens, windows, h_kv, h, d, e=2):
@@ -301,7 +397,7 @@ def run_c3(dev, stream, steps, kps=0, ckps=0):
                                     keys_per_split=ckps)
         src.cache_seqlens.add_(P)
 
-    ms_prefill = _graph_time(stream, prefill_body, lambda: src.cache_seqlens.zero_(), reps=5)
+    ms_prefill = _graph_time(stream, prefill_body, lambda: src.cache_seqlens.zero_())
     a = _ext.FanoutArgs()
     a.k_src, a.v_src = src.k_cache.data_ptr(), src.v_cache.data_ptr()
     a.k_dst, a.v_dst = dst.k_cache.data_ptr(), dst.v_cache.data_ptr()
@@ -313,7 +409,7 @@ def run_c3(dev, stream, steps, kps=0, ckps=0):
     def fanout_body():
         _ext.check(_ext.lib().nc_kv_fanout(ctypes.byref(a), torch.cuda.current_stream().cuda_stream), "fanout")
 
-    ms_fan = _graph_time(stream, fanout_body, lambda: None, reps=10)
+    ms_fan = _graph_time(stream, fanout_body, lambda: None)
 
     def decode_body():
         for i in range(steps):
@@ -510,8 +606,8 @@ def run_paged(dev, stream, steps, kps=0, ckps=0, page=256):
                                         keys_per_split=ckps)
         return run
 
-    ms_chunk_dense = _graph_time(stream, chunk_body(False), reset, reps=steps)
-    ms_chunk_paged = _graph_time(stream, chunk_body(True), reset, reps=steps)
+    ms_chunk_dense = _graph_time(stream, chunk_body(False), reset)
+    ms_chunk_paged = _graph_time(stream, chunk_body(True), reset)
     return {"config": "paged", "workload": f"C2 decode (d20, B=32, 20 layers) through {page}-token pages of a "
                                            f"shuffled pool vs the dense cache, {steps} steps; and one "
                                            f"{tc}-token chunk per row into the same caches, 20 layers",
@@ -596,21 +692,49 @@ def run_head(dev, stream, steps, kps=0, ckps=0):
             "fused_head_TBps": round(head_bytes / (res["fused_head_us"] * 1e-6) / 1e12, 3)}
 
 
+def _profile_value(name: str, key: str):
+    """A figure recorded in a committed rocprofv3 summary (profiles/<name>) as a `key: value` line."""
+    path = ROOT / "profiles" / name
+    if not path.exists():
+        return None
+    m = re.search(r"^%s:\s*([0-9.eE+-]+)\s*$" % re.escape(key), path.read_text(), flags=re.M)
+    return float(m.group(1)) if m else None
+
+
+def other_configs(dev, stream) -> dict:
+    """C3, C4 and C5 figures for the metric line (same kernels and method, bounded step counts)."""
+    out = {}
+    for name, fn, steps in (("c3", run_c3, 32), ("c4", run_c4, 64), ("c5", run_c5, 8)):
+        t0 = time.perf_counter()
+        res = fn(dev, stream, steps)
+        res.pop("config", None)
+        out[name] = res
+        torch.cuda.empty_cache()
+        log(f"[bench] {name}: {json.dumps(res)} ({time.perf_counter() - t0:.1f} s)")
+    out["c3"]["prefill_mfma_busy_pct"] = _profile_value("attn_chunk_d24_prefill_pmc.md", "mfma_busy_pct")
+    out["c5"]["chunk_mfma_busy_pct"] = _profile_value("attn_gqa_mixed_c5_pmc.md", "mfma_busy_pct")
+    out["mfma_busy_source"] = ("SQ_VALU_MFMA_BUSY_CYCLES / (kernel duration x clock x SIMDs) from the committed "
+                               "rocprofv3 --pmc summaries in profiles/ (counters cannot be read inside this run)")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--replays", type=int, default=REPLAYS, help="timed graph replays (median reported), >= 20")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--keys-per-split", type=int, default=0,
                     help="decode split size (multiple of 64; 0 = library default)")
     ap.add_argument("--chunk-keys-per-split", type=int, default=0,
                     help="c3/c5 chunk-kernel split size (0 = library default)")
-    ap.add_argument("--eager", action="store_true", help="also time the steps without a graph")
+    ap.add_argument("--no-eager", action="store_true", help="skip the eager (un-captured) timing of the C2 steps")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C3/C4/C5 figures of the metric line")
     ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4", "c5", "e2e", "head", "paged"],
-                    help="c2 (default) is the metric line; c3/c4/c5 print per-phase figures; e2e times the d20 "
-                         "model's decode step; head the fused logits head and the sampler; paged C2 through "
-                         "a page table")
+                    help="c2 (default) is the metric line (with C3/C4/C5 figures); c3/c4/c5 print one config's "
+                         "figures; e2e times the d20 model's decode step; head the fused logits head and the "
+                         "sampler; paged C2 through a page table")
     ap.add_argument("--rope", action="store_true",
                     help="c2 through flash_attn_with_kvcache_rope (QK prologue fused; same bytes + tables)")
     args = ap.parse_args()
@@ -635,6 +759,7 @@ def main() -> int:
     if args.steps < 1 or args.steps > T_MAX - S_HI:
         print(f"bench.py: --steps must be in [1, {T_MAX - S_HI}] (cache capacity {T_MAX})", file=sys.stderr)
         return 2
+    reps = max(20, args.replays)
 
     from nanochat_amd import _ext
     from nanochat_amd.flash_attention import flash_attn_with_kvcache
@@ -646,7 +771,7 @@ def main() -> int:
     s0 = c2_seqlens()
     K, W = args.steps, args.warmup
     log(f"[bench] C2 d20 decode: L={LAYERS} B={BATCH} H={HEADS}/{KV_HEADS} D={HEAD_DIM} T_max={T_MAX} "
-        f"steps={K} warmup={W} s0 mean={s0.float().mean():.1f}")
+        f"steps={K} warmup={W} replays={reps} s0 mean={s0.float().mean():.1f}")
 
     with torch.cuda.stream(stream):
         gd = torch.Generator(device=dev)
@@ -683,7 +808,8 @@ def main() -> int:
         for i in range(W):
             one_step(i)
         eager_ms = None
-        if args.eager:
+        if not args.no_eager:
+            # the same K steps without a graph: Python dispatch of every call included (wall clock)
             seqlens.copy_(s0_dev)
             stream.synchronize()
             t0 = time.perf_counter()
@@ -700,26 +826,26 @@ def main() -> int:
             one_step(i)
     log(f"[bench] captured {K} steps ({K * LAYERS} decode launches) in one HIP graph")
 
+    reset = lambda: seqlens.copy_(s0_dev)  # noqa: E731
     with torch.cuda.stream(stream):
-        # untimed replay, then restore the starting positions
+        # untimed replay; then one replay bracketed by synchronisation on both sides (wall clock)
+        reset()
         graph.replay()
-        seqlens.copy_(s0_dev)
+        reset()
         stream.synchronize()
         torch.cuda.synchronize()
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
-        ev0.record(stream)
         graph.replay()
-        ev1.record(stream)
         stream.synchronize()
         torch.cuda.synchronize()
         wall_s = time.perf_counter() - t0
-        gpu_ms = ev0.elapsed_time(ev1)
-        final_seq = seqlens.cpu()
+    # the timed replays: HIP events on the launch stream around each replay; the median is the figure
+    times = _replay_times(stream, graph, reset, reps)
+    final_seq = seqlens.cpu()
     if not torch.equal(final_seq, s0 + K):
         log(f"[bench] ERROR: positions after the timed region are wrong: {final_seq[:4]} vs {(s0 + K)[:4]}")
         return 1
+    gpu_ms = statistics.median(times)
 
     total_bytes = sum(step_bytes(s0 + i) for i in range(K))
     t_s = gpu_ms / 1e3
@@ -728,8 +854,18 @@ def main() -> int:
     launches = K * LAYERS
     avg_launch_us = gpu_ms * 1e3 / launches
     bytes_per_launch = total_bytes / launches
-    log(f"[bench] graph replay: {gpu_ms:.3f} ms (HIP events), {wall_s * 1e3:.3f} ms wall; "
-        f"{ms_per_step:.4f} ms/step; {gbps:.1f} GB/s; eager {eager_ms} ms/step")
+    log(f"[bench] graph replays: median {gpu_ms:.3f} ms (min {min(times):.3f}, max {max(times):.3f}, {reps} "
+        f"replays, HIP events), one synchronised replay {wall_s * 1e3:.3f} ms wall; {ms_per_step:.4f} ms/step; "
+        f"{gbps:.1f} GB/s; eager {eager_ms} ms/step")
+
+    seqlens.copy_(s0_dev)
+    ceil = read_ceilings(dev, stream, k_cache[0], v_cache[0], seqlens, bytes_per_launch)
+    ceil["copy_rw_GBps"] = round(copy_ceiling(dev, stream), 1)
+    log(f"[bench] ceilings: {ceil}")
+    del graph, k_cache, v_cache, q_all, k_all, v_all
+    torch.cuda.empty_cache()
+
+    configs = None if args.no_configs else other_configs(dev, stream)
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -737,8 +873,6 @@ def main() -> int:
         cpu = cpu_baseline(args.cpu_seconds)
         log(f"[bench] CPU baseline: {cpu}")
 
-    copy_gbps = copy_ceiling(dev, stream)
-    log(f"[bench] torch copy_ of 2 GiB: {copy_gbps:.0f} GB/s (read + write)")
     traffic = read_traffic()
     out = {
         "metric": METRIC,
@@ -757,14 +891,19 @@ def main() -> int:
             "workload": "C2: d20 decode, flash_attn_with_kvcache append+attention, 20 layers x 10/10 heads x 128, "
                         "B=32, T_max=2304, window (-1,0), one token per row per layer per step",
             "layers": LAYERS, "batch": BATCH, "heads": HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
-            "cache_len": T_MAX, "timing": "HIP graph of all steps, HIP events on the launch stream",
+            "cache_len": T_MAX, "s0_mean": round(float(s0.float().mean()), 2),
+            "timing": f"HIP graph of all {K} steps; median of {reps} replays timed with HIP events on the launch "
+                      f"stream (positions reset between replays, outside the events)",
         },
         "pct_of_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
-        "hbm_copy_gbps": round(copy_gbps, 1),
-        "pct_of_copy": round(100.0 * gbps / copy_gbps, 2),
         "tokens_per_s": round(BATCH * K / t_s, 1),
+        "replay_ms": {"median": round(gpu_ms, 4), "min": round(min(times), 4), "max": round(max(times), 4),
+                      "replays": reps},
         "wall_ms_per_step": round(wall_s * 1e3 / K, 5),
         "eager_ms_per_step": round(eager_ms, 5) if eager_ms is not None else None,
+        "ceilings": ceil,
+        "pct_of_read_linear": round(100.0 * gbps / ceil["read_linear_GBps"], 2),
+        "pct_of_read_c2_shape": round(100.0 * gbps / ceil["read_c2_shape_GBps"], 2),
         "roofline": {
             "bound": "hbm",
             "achieved": round(bytes_per_launch / (avg_launch_us * 1e-6) / 1e9, 2),
@@ -773,11 +912,12 @@ def main() -> int:
             "frac": round(bytes_per_launch / (avg_launch_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
             "traffic": traffic[0] if traffic else None,
             "traffic_over_algorithmic": round(traffic[0] / traffic[1], 4) if traffic else None,
-            "kernel": "one flash_attn_with_kvcache decode call: decode_attn_kernel<bf16, packed-q, D=128, GB=1> "
-                      "(fused append + split-K) + merge_splits_kernel<128, 1>",
+            "kernel": "one flash_attn_with_kvcache decode call (C2 layer): decode_attn_kernel<bf16, packed-q, "
+                      "D=128, GB=1> with the fused append and split-K merge",
             "avg_launch_us": round(avg_launch_us, 3),
             "algorithmic_bytes_per_launch": round(bytes_per_launch),
         },
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

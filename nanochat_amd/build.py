@@ -20,6 +20,9 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libnc_kv.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+# measurement tooling for bench.py (read-bandwidth ceilings); not part of the KV-cache library
+PROBE_SOURCE = "probe.hip"
+PROBE_PATH = PKG_DIR / "libnc_probe.so"
 OBJ_DIR = PKG_DIR / "_build"
 ARCH = "gfx950"
 
@@ -86,7 +89,24 @@ def build(verbose: bool = True, defines: dict | None = None, out: Path | None = 
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}", flush=True)
+    if not extra and out == LIB_PATH:
+        build_probe(verbose)
     return out
+
+
+def build_probe(verbose: bool = True) -> Path:
+    """Compile bench.py's read-bandwidth probes into nanochat_amd/libnc_probe.so."""
+    OBJ_DIR.mkdir(parents=True, exist_ok=True)
+    obj = _compile(PROBE_SOURCE, OBJ_DIR, ())
+    tmp = PROBE_PATH.with_suffix(".so.tmp")
+    res = subprocess.run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), str(obj)],
+                         capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    os.replace(tmp, PROBE_PATH)
+    if verbose:
+        print(f"built {PROBE_PATH}", flush=True)
+    return PROBE_PATH
 
 
 if __name__ == "__main__":
