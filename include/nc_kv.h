@@ -190,7 +190,7 @@ typedef struct nc_attn_args {
   int64_t v_stride_b, v_stride_t, v_stride_h;
   int32_t window_left;           /* < 0: unlimited */
   int32_t causal;
-  float softmax_scale;           /* nanochat: head_dim ** -0.5 */
+  float softmax_scale;           /* > 0, finite (nanochat: head_dim ** -0.5) */
   int32_t q_dtype;               /* dtype of q, k, v and out */
   int32_t cache_dtype;
   int32_t keys_per_split;        /* keys one workgroup covers before a split-K merge;

@@ -10,17 +10,31 @@
 // Positions outside [0, t_max) are not stored and set NC_DEVERR_OVERFLOW,
 // as the standalone append does.
 //
-// Tiling.  A workgroup owns 64 "rows" = (query, q head) pairs of one
-// (row b, kv head, q-head block): 64 / GB queries x GB heads, so the GB heads
-// that share a kv head read each K/V tile once.  4 waves x 16 rows.  Key tiles
-// of 64 positions are staged in LDS as [key][dim] rows (16-byte stores), padded
-// so the MFMA operand reads are bank-conflict free.
+// Tiling.  A workgroup owns ROWS = 64 or 128 "rows" = (query, q head) pairs of
+// one (row b, kv head, q-head block): ROWS / GB queries x GB heads, so the GB
+// heads that share a kv head read each K/V tile once.  8 waves: with 128 rows
+// each wave owns 16 rows and scores whole 64-key tiles; with 64 rows (calls of
+// few workgroups) two groups of 4 waves take the two 32-key halves of every
+// tile for the same rows and merge their (m, l, o) in LDS at the end.
+//
+// K/V tiles go through a ring of LDS stages filled by direct loads
+// (global_load_lds_dwordx4: no registers, no LDS store instructions), the next
+// tile in flight while the current one is consumed.  Tile rows are unpadded
+// 256-byte rows whose 16-byte chunks sit in slots chunk ^ swz(row), chosen on
+// the global side of the load, so the MFMA operand reads hit all 64 banks.
+// The waits are counted: every lane issues every load (lanes past the span or
+// outside the page pool read a valid key, zeroed once landed), so a wave has a
+// fixed number of loads per tile in flight, and each stage is a separate
+// __shared__ array named statically at every access (the compiler then sees
+// that a stage being filled is not the one being read).
 //
 // Per tile and wave (v_mfma_f32_16x16x32_{bf16,f16}; lane l, q = l / 16):
 //   S^T = K . Q^T   A = K[16 keys][32 dims] (LDS), B = Q^T (registers);
 //                   lane l holds S[row l%16][keys 16kb + 4q + r], r < 4.
-//   softmax         each lane owns one query row: running max / sum in fp32,
-//                   cross-lane reductions over the 4 lane groups only.
+//   softmax         each lane owns one query row: running max / sum in fp32
+//                   (maxima of the unscaled scores, the scale folded into the
+//                   exponent's fma), cross-lane reductions over the 4 lane
+//                   groups only.
 //   O^T += V^T . P^T  B = P^T straight from the S registers (the 32 keys of a
 //                   chunk are enumerated in the order the lanes hold them), so
 //                   P never leaves registers.  A = V^T in that same key order
@@ -37,11 +51,11 @@
 // A span that fits one split writes the output directly; otherwise each split
 // writes (o, m, l) partials per (query, head) and the split-merge kernel of
 // the decode path combines them (chunk_span gives both sides the same split
-// count; workgroups past it return at once).  The next key tile is
-// loaded into registers while the current one is consumed from LDS.
+// count; workgroups past it return at once).
 
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "nc_kv_common.hpp"
 #include "nc_kv_internal.hpp"
@@ -50,9 +64,20 @@ namespace nckv {
 
 namespace {
 
-constexpr int kChunkWaves = 4;
-constexpr int kRows = 64;        // (query, head) rows per workgroup
-constexpr int kBN = 64;          // keys per tile
+// Every workgroup has 8 waves.  With ROWS = 128 each wave owns 16 of the rows
+// and scores whole key tiles; with ROWS = 64, two wave groups of 4 split every
+// key tile: group g scores keys [g, g + 1) * kBN / 2 of each tile for the same
+// 64 rows, and the groups' (m, l, o) meet in LDS at the end (twice the waves of
+// a 4-wave workgroup, to hide latency, without more LDS).
+constexpr int kChunkWaves = 8;
+#ifndef NC_CHUNK_TILE_KEYS
+#define NC_CHUNK_TILE_KEYS 64
+#endif
+#ifndef NC_CHUNK_STAGES
+#define NC_CHUNK_STAGES 2
+#endif
+constexpr int kBN = NC_CHUNK_TILE_KEYS;   // keys per tile (a multiple of 32)
+constexpr int kStages = NC_CHUNK_STAGES;  // K/V tiles of the LDS ring (>= 2): kStages - 1 in flight
 constexpr int kChunkStagePages = 512;  // page numbers a workgroup stages in LDS (paged cache)
 constexpr float kNegBigC = -1.0e30f;
 constexpr int kXcdsC = 8;
@@ -64,6 +89,35 @@ typedef __attribute__((address_space(3))) char lds_char;
 // ds_read_b64_tr_b16 from a generic pointer into a __shared__ array.
 __device__ __forceinline__ i16x4 lds_read_tr16(const char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((lds_char*)(p)));
+}
+
+typedef __attribute__((address_space(1))) const void global_cvoid;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One wave's 16-byte direct load into LDS (global_load_lds_dwordx4): lane l's
+// 16 bytes from `src` land at dst + 16 * l.  `dst` must be wave-uniform.  The
+// load counts in the wave's vector-memory counter like any other load.
+__device__ __forceinline__ void dma16(const char* src, char* dst) {
+  __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)((lds_char*)dst), 16, 0, 0);
+}
+
+// Wait until at most N of this wave's vector-memory operations are outstanding
+// (s_waitcnt vmcnt(N); expcnt and lgkmcnt left alone).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// LDS layout of a K or V tile: key row r holds its CPR 16-byte chunks in
+// slots permuted by chunk ^ swz(r), so that the MFMA operand reads (8 rows x
+// 16 bytes of one chunk per phase for K; 4 rows x 2 chunks, 8 bytes each,
+// per 16 lanes for the transposed V reads) spread over all 64 banks.
+template <int CPR>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (CPR == 16) return 2 * (r & 7);
+  else if constexpr (CPR == 8) return 2 * ((r >> 1) & 3);
+  else return 0;
 }
 
 struct ChunkParams {
@@ -137,20 +191,43 @@ template <> struct mfma_t<f16> {
 // LK: 0 plain launch, with no lookup code (it cost 3% on the C5 batch); 1
 // cache_batch_idx / cu_seqlens_q lookups; 2 those and a page table (kernels of
 // their own, so the lookup kernels keep their code).
-template <typename TC, int D, int GB, int LK>
-__global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const ChunkParams p) {
+#ifndef NC_CHUNK_WAVES_PER_EU
+#define NC_CHUNK_WAVES_PER_EU 4  // > 0: register budget for this many waves per SIMD
+#endif
+#if NC_CHUNK_WAVES_PER_EU > 0
+#define NC_CHUNK_OCC __attribute__((amdgpu_waves_per_eu(NC_CHUNK_WAVES_PER_EU)))
+#else
+#define NC_CHUNK_OCC
+#endif
+
+template <typename TC, int D, int GB, int LK, int ROWS>
+__global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_kernel(const ChunkParams p) {
   typedef typename mfma_t<TC>::v8 v8;
-  constexpr int QB = kRows / GB;          // queries per workgroup
+  constexpr int kRowWaves = ROWS / 16;    // waves covering the rows, 16 each
+  constexpr int kKeyGroups = kChunkWaves / kRowWaves;  // wave groups splitting each key tile
+  static_assert(kRowWaves * kKeyGroups == kChunkWaves && (kKeyGroups == 1 || kKeyGroups == 2), "rows");
+  constexpr int QB = ROWS / GB;           // queries per workgroup
   constexpr int DC = D / 32;              // 32-dim chunks (MFMA K for S)
   constexpr int DB = D / 16;              // 16-dim output blocks
-  constexpr int KROW = D * 2 + 16;        // bytes per K row in LDS (padded: 16-byte reads, 8 lanes/cycle)
-  constexpr int VROW = D * 2 + 32;        // bytes per V row in LDS (padded: transpose reads, 16 lanes/cycle)
-  constexpr int CHUNKS = kBN * D / 8;     // 16-byte chunks per tile (K or V)
-  constexpr int PER_THREAD = CHUNKS / (kChunkWaves * kWave);
-  static_assert(PER_THREAD * kChunkWaves * kWave == CHUNKS, "tile / workgroup shape");
+  constexpr int KG = kBN / kKeyGroups;    // keys of a tile one wave group scores
+  constexpr int KB = KG / 16;             // 16-key blocks per wave and tile (S MFMAs)
+  constexpr int KC = KG / 32;             // 32-key chunks per wave and tile (P.V MFMAs)
+  constexpr int CPR = D / 8;              // 16-byte chunks per key row
+  constexpr int ROWB = D * 2;             // bytes per key row in LDS (unpadded, swizzled)
+  constexpr int TILEB = kBN * ROWB;       // bytes of a K (or V) tile
+  constexpr int NI = kBN * CPR / kWave / kChunkWaves;  // direct loads per wave per tile, K (V the same)
+  constexpr int LPT = 2 * NI;             // vector-memory operations per wave per tile
+  static_assert(NI * kWave * kChunkWaves == kBN * CPR && KG % 32 == 0, "tile / workgroup shape");
+  static_assert(kStages >= 2 && (kStages - 2) * LPT < 64, "ring depth");
 
-  __shared__ __attribute__((aligned(16))) char ks[kBN * KROW];
-  __shared__ __attribute__((aligned(16))) char vs[kBN * VROW];
+  // ring of kStages tiles, one __shared__ array per stage (K at [0], V at [1]):
+  // every access below names its stage statically, so the compiler can tell a
+  // stage being filled by direct loads from the stage being read
+  static_assert(kStages <= 4, "ring stages");
+  __shared__ __attribute__((aligned(1024))) char ring0[2][TILEB];
+  __shared__ __attribute__((aligned(1024))) char ring1[2][TILEB];
+  __shared__ __attribute__((aligned(1024))) char ring2[kStages > 2 ? 2 : 1][kStages > 2 ? TILEB : 16];
+  __shared__ __attribute__((aligned(1024))) char ring3[kStages > 3 ? 2 : 1][kStages > 3 ? TILEB : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -159,6 +236,9 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lq = lane / 16;               // lane group 0..3
   const int lr = lane % 16;
+  const int rw = wave % kRowWaves;        // row block of this wave
+  const int kg = wave / kRowWaves;        // key group of this wave
+  const int kgo = kg * KG;                // its first key within a tile
 
   // ---- block -> (group = (b, kv head, head block), key split, q tile) ----
   // A group's blocks run on one XCD (workgroups go round-robin over the 8 XCDs)
@@ -204,7 +284,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   }
 
   // this lane's query row
-  const int row = wave * 16 + lr;
+  const int row = rw * 16 + lr;
   const int qi = q0 + row / GB;
   const int h = hk * p.group + hb * GB + row % GB;
   const bool row_ok = qi < rq.len;
@@ -253,19 +333,15 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   const int64_t knst = p.k_st * EB;
   const int64_t vnst = p.v_st * EB;
 
-  // ---- key tiles: registers hold the next tile while the current one is
-  // consumed from LDS (a second register stage measured no faster) ----
-  // Thread chunk u of a tile is key key0 + u * KSTEP, 16-byte column dc0 (the
-  // plan keeps a tile's byte span below 2^31, so offsets are 32-bit).
-  constexpr int CPR = D / 8;                          // 16-byte chunks per key row
-  constexpr int KSTEP = kChunkWaves * kWave / CPR;    // keys between a thread's chunks
-  const int key0 = tid / CPR, dc0 = tid % CPR;
-  uint32_t koff[PER_THREAD], voff[PER_THREAD];
-#pragma unroll
-  for (int u = 0; u < PER_THREAD; ++u) {
-    koff[u] = static_cast<uint32_t>((key0 + u * KSTEP) * kst + dc0 * 16);
-    voff[u] = static_cast<uint32_t>((key0 + u * KSTEP) * vst + dc0 * 16);
-  }
+  // ---- key tiles: a ring of kStages LDS tiles filled by direct loads, kStages - 1 tiles ahead ----
+  // Load slot i of this wave covers the 64 16-byte LDS chunks [64 n, 64 n + 64) of a tile,
+  // n = wave * NI + i: key row lrow[i], holding global chunk (chunk slot ^ swz(row)) at byte
+  // column lcol[i] (the plan keeps a tile's byte span below 2^31, so offsets are 32-bit).
+  constexpr int RPI = kWave / CPR;        // key rows one direct load covers
+  auto lrow = [&](int i) __attribute__((always_inline)) { return (wave * NI + i) * RPI + lane / CPR; };
+  auto lcol = [&](int i) __attribute__((always_inline)) {
+    return static_cast<uint32_t>(((lane % CPR) ^ swz<CPR>(lrow(i))) * 16);
+  };
   // paged cache: the page numbers of this workgroup's keys [lo, hi), read from
   // the table once into LDS (entries outside the pool become -1 and set
   // NC_DEVERR_PAGE), so a tile's K/V loads wait on LDS rather than on a table
@@ -274,26 +350,36 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   // their stores look pages up, and a staging prologue would only add latency).
   [[maybe_unused]] int page_lo = 0;
   [[maybe_unused]] bool pages_staged = false;
+  [[maybe_unused]] bool pages_bad = false;
   [[maybe_unused]] const int32_t* sm_pg = nullptr;
   if constexpr (LK == 2) {
     __shared__ int32_t sm_pages[kChunkStagePages];
+    __shared__ int sm_bad;
     page_lo = lo >> p.pages.shift;
     const int npages = hi > lo ? ((hi - 1) >> p.pages.shift) - page_lo + 1 : 0;
     pages_staged = npages <= kChunkStagePages && min(hi, new_lo) > lo;
     if (pages_staged) {
+      if (tid == 0) sm_bad = 0;
+      __syncthreads();
       for (int i = tid; i < npages; i += kChunkWaves * kWave) {
         const int32_t blk = p.pages.table[b * p.pages.stride + page_lo + i];
         const bool ok = blk >= 0 && blk < p.pages.n_blocks;
-        if (!ok && p.err != nullptr) atomicOr(p.err, NC_DEVERR_PAGE);
+        if (!ok) {
+          sm_bad = 1;
+          if (p.err != nullptr) atomicOr(p.err, NC_DEVERR_PAGE);
+        }
         sm_pages[i] = ok ? blk : -1;
       }
       __syncthreads();
+      pages_bad = sm_bad != 0;
+    } else {
+      pages_bad = true;  // per-key lookups: any tile may hold a key outside the pool
     }
     sm_pg = sm_pages;
   }
   // physical cache position of logical key j in [lo, hi): j, or its page-table
   // slot (-1: not addressable)
-  auto cache_pos = [&](int j) -> int64_t {
+  auto cache_pos = [&](int j) __attribute__((always_inline)) -> int64_t {
     if constexpr (LK == 2) {
       if (pages_staged) {
         const int32_t blk = sm_pg[(j >> p.pages.shift) - page_lo];
@@ -304,104 +390,80 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     return j;
   };
   constexpr bool contiguous = LK != 2;  // positions are cache rows (no page table)
-  uint4 kreg[PER_THREAD], vreg[PER_THREAD];
-  auto load_regs = [&](int kt0, uint4 (&kr)[PER_THREAD], uint4 (&vr)[PER_THREAD]) {
+  // Issue tile t's direct loads into its ring stage.  Every lane issues every
+  // load (so each wave always has LPT operations per tile in flight, which the
+  // waits below count on): keys past the span read the span's last key and
+  // keys outside the page pool read block 0, and both are zeroed once landed.
+  const int ntiles = hi > lo ? (hi - lo + kBN - 1) / kBN : 0;
+  // the K and V tiles of ring stage st (a compile-time index at every use)
+  auto stage_k = [&](auto st) __attribute__((always_inline)) -> char* {
+    constexpr int S = decltype(st)::value;
+    if constexpr (S == 0) return ring0[0]; else if constexpr (S == 1) return ring1[0];
+    else if constexpr (S == 2) return ring2[0]; else return ring3[0];
+  };
+  auto stage_v = [&](auto st) __attribute__((always_inline)) -> char* {
+    constexpr int S = decltype(st)::value;
+    if constexpr (S == 0) return ring0[1]; else if constexpr (S == 1) return ring1[1];
+    else if constexpr (S == 2) return ring2[1]; else return ring3[1];
+  };
+  auto issue = [&](int t, auto st) __attribute__((always_inline)) {
+    const int kt0 = lo + t * kBN;
+    char* kd = stage_k(st) + wave * NI * kWave * 16;
+    char* vd = stage_v(st) + wave * NI * kWave * 16;
     if (contiguous && kt0 + kBN <= hi && kt0 + kBN <= new_lo) {
-      // whole tile inside the span and in the cache: no per-chunk checks
+      // whole tile inside the span and in the cache: no per-key checks
       const char* kt = kbase + kt0 * kst;
       const char* vt = vbase + kt0 * vst;
 #pragma unroll
-      for (int u = 0; u < PER_THREAD; ++u) {
-        kr[u] = *reinterpret_cast<const uint4*>(kt + koff[u]);
-        vr[u] = *reinterpret_cast<const uint4*>(vt + voff[u]);
-      }
-      return;
-    }
-    if (!contiguous) {  // paged cache: each cached key's slot from the page table
-      if (pages_staged && kt0 + kBN <= hi && kt0 + kBN <= new_lo) {
-        // whole tile in the cache: branch-free loads (a key of a page outside
-        // the pool reads block 0, which exists, and is then zeroed)
-        const int pmask = (1 << p.pages.shift) - 1;
-#pragma unroll
-        for (int u = 0; u < PER_THREAD; ++u) {
-          const int j = kt0 + key0 + u * KSTEP;
-          const int32_t blk = sm_pg[(j >> p.pages.shift) - page_lo];
-          const int64_t pj = (static_cast<int64_t>(max(blk, 0)) << p.pages.shift) | (j & pmask);
-          const uint4 kx = *reinterpret_cast<const uint4*>(kbase + pj * kst + dc0 * 16);
-          const uint4 vx = *reinterpret_cast<const uint4*>(vbase + pj * vst + dc0 * 16);
-          kr[u] = blk >= 0 ? kx : make_uint4(0, 0, 0, 0);
-          vr[u] = blk >= 0 ? vx : make_uint4(0, 0, 0, 0);
-        }
-        return;
-      }
-#pragma unroll
-      for (int u = 0; u < PER_THREAD; ++u) {
-        const int j = kt0 + key0 + u * KSTEP;
-        const bool from_new = j >= new_lo;
-        const int64_t pj = (j < hi && !from_new) ? cache_pos(j) : 0;
-        if (j < hi && pj >= 0) {
-          const char* kp = from_new ? knew + (j - s) * knst : kbase + pj * kst;
-          const char* vp = from_new ? vnew + (j - s) * vnst : vbase + pj * vst;
-          kr[u] = *reinterpret_cast<const uint4*>(kp + dc0 * 16);
-          vr[u] = *reinterpret_cast<const uint4*>(vp + dc0 * 16);
-        } else {
-          kr[u] = make_uint4(0, 0, 0, 0);
-          vr[u] = make_uint4(0, 0, 0, 0);
-        }
+      for (int i = 0; i < NI; ++i) {
+        dma16(kt + (static_cast<uint32_t>(lrow(i) * kst) + lcol(i)), kd + i * kWave * 16);
+        dma16(vt + (static_cast<uint32_t>(lrow(i) * vst) + lcol(i)), vd + i * kWave * 16);
       }
       return;
     }
 #pragma unroll
-    for (int u = 0; u < PER_THREAD; ++u) {
-      const int j = kt0 + key0 + u * KSTEP;
-      if (j < hi) {
-        const bool from_new = j >= new_lo;
-        const char* kp = from_new ? knew + (j - s) * knst : kbase + j * kst;
-        const char* vp = from_new ? vnew + (j - s) * vnst : vbase + j * vst;
-        kr[u] = *reinterpret_cast<const uint4*>(kp + dc0 * 16);
-        vr[u] = *reinterpret_cast<const uint4*>(vp + dc0 * 16);
+    for (int i = 0; i < NI; ++i) {
+      const int j = min(kt0 + lrow(i), hi - 1);
+      const char* ks_;
+      const char* vs_;
+      if (j >= new_lo) {
+        ks_ = knew + (j - s) * knst;
+        vs_ = vnew + (j - s) * vnst;
       } else {
-        kr[u] = make_uint4(0, 0, 0, 0);
-        vr[u] = make_uint4(0, 0, 0, 0);
+        const int64_t pj = contiguous ? j : max(cache_pos(j), int64_t(0));
+        ks_ = kbase + pj * kst;
+        vs_ = vbase + pj * vst;
       }
+      dma16(ks_ + lcol(i), kd + i * kWave * 16);
+      dma16(vs_ + lcol(i), vd + i * kWave * 16);
     }
   };
+
   // wave-uniform bounds of this wave's query rows: tiles wholly inside every
   // row's mask skip the per-element mask
-  const int qi_first = q0 + (wave * 16) / GB, qi_last = q0 + (wave * 16 + 15) / GB;
+  const int qi_first = q0 + (rw * 16) / GB, qi_last = q0 + (rw * 16 + 15) / GB;
   const bool wave_rows_full = qi_last < rq.len;
   const int qpos_first = s + qi_first, qpos_last = s + qi_last;
-  auto tile_step = [&](int kt0, uint4 (&kr)[PER_THREAD], uint4 (&vr)[PER_THREAD]) {
-    __syncthreads();  // previous tile's LDS reads are done
-#pragma unroll
-    for (int u = 0; u < PER_THREAD; ++u) {
-      const int key = key0 + u * KSTEP;
-      *reinterpret_cast<uint4*>(ks + key * KROW + dc0 * 16) = kr[u];
-      *reinterpret_cast<uint4*>(vs + key * VROW + dc0 * 16) = vr[u];
-    }
-    if (kt0 + kBN > own_lo) {  // the tile holds new tokens this workgroup stores
-#pragma unroll
-      for (int u = 0; u < PER_THREAD; ++u) {
-        const int j = kt0 + key0 + u * KSTEP;
-        const bool own = j >= own_lo && j < hi;
-        const int64_t pj = own ? (contiguous ? j : cache_pos(j)) : -1;
-        if (pj >= 0) {
-          *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + pj * kst + dc0 * 16) = kr[u];
-          *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + pj * vst + dc0 * 16) = vr[u];
-        }
-      }
-    }
-    __syncthreads();
-    if (kt0 + kBN < hi) load_regs(kt0 + kBN, kr, vr);
+  // this lane's LDS read offsets (the swizzle depends only on the row within a 16-row block):
+  // K chunk (4c + lq) of row lr; V row 4 lq + lr / 4 of a 32-key chunk (the +16 half has the
+  // same swizzle), 8 bytes at dims 16 db + 4 (lr % 4)
+  const int k_sw = swz<CPR>(lr);
+  const int v_row = 4 * lq + lr / 4;
+  const int v_sw = swz<CPR>(v_row);
+  auto k_rd = [&](int c) __attribute__((always_inline)) { return lr * ROWB + (((4 * c + lq) ^ k_sw) * 16); };
+  auto v_rd = [&](int db) __attribute__((always_inline)) {
+    return v_row * ROWB + (((2 * db + (lr % 4) / 2) ^ v_sw) * 16) + ((lr % 4) % 2) * 8;
+  };
 
-    // ---- S^T = K . Q^T for the 4 key blocks of the tile ----
-    f4v acc_s[4];
+  auto compute = [&](int kt0, const char* ks, const char* vs) __attribute__((always_inline)) {
+    // ---- S^T = K . Q^T for the KB key blocks of the tile ----
+    f4v acc_s[KB];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       acc_s[kb] = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < DC; ++c) {
-        const uint4 a = *reinterpret_cast<const uint4*>(ks + (16 * kb + lr) * KROW + (32 * c + 8 * lq) * 2);
+        const uint4 a = *reinterpret_cast<const uint4*>(ks + (kgo + 16 * kb) * ROWB + k_rd(c));
         mfma_t<TC>::run(__builtin_bit_cast(v8, a), qf[c], acc_s[kb]);
       }
     }
@@ -409,16 +471,18 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     // ---- mask, scale, online softmax (each lane: one query row) ----
     const bool interior = wave_rows_full && kt0 + kBN <= hi && kt0 + kBN - 1 <= qpos_first &&
                           (p.window < 0 || kt0 >= qpos_last - p.window);
-    float sv[4][4];
+    // raw scores (the scale is positive: the running max is taken before scaling
+    // and the scale folded into the exponent's fma)
+    float sv[KB][4];
     float mt = -__builtin_inff();
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       const float a4[4] = {acc_s[kb][0], acc_s[kb][1], acc_s[kb][2], acc_s[kb][3]};
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sv[kb][r] = a4[r] * p.scale_log2;
+        sv[kb][r] = a4[r];
         if (!interior) {
-          const int j = kt0 + 16 * kb + 4 * lq + r;
+          const int j = kt0 + kgo + 16 * kb + 4 * lq + r;
           const bool ok = row_ok && j >= row_lo && j <= qpos && j < hi;
           sv[kb][r] = ok ? sv[kb][r] : -__builtin_inff();
         }
@@ -427,16 +491,16 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     }
     mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
     mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float m_new = fmaxf(m_run, mt);
+    const float m_new = fmaxf(m_run, mt * p.scale_log2);
     const float alpha = fast_exp2(m_run - m_new);
     float rs = 0.0f;
-    uint32_t pk[4][2];  // P packed in the cache dtype: [key block][pair of r]
+    uint32_t pk[KB][2];  // P packed in the cache dtype: [key block][pair of r]
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       float pv[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pv[r] = fast_exp2(sv[kb][r] - m_new);
+        pv[r] = fast_exp2(__builtin_fmaf(sv[kb][r], p.scale_log2, -m_new));
         rs += pv[r];
       }
       pk[kb][0] = mfma_t<TC>::pack2(pv[0], pv[1]);
@@ -454,25 +518,107 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
     }
     m_run = m_new;
 
-    // ---- O^T += V^T . P^T over the two 32-key chunks ----
+    // ---- O^T += V^T . P^T over the KC 32-key chunks ----
 #pragma unroll
-    for (int kc = 0; kc < 2; ++kc) {
+    for (int kc = 0; kc < KC; ++kc) {
       const v8 bp = __builtin_bit_cast(v8, make_uint4(pk[2 * kc][0], pk[2 * kc][1], pk[2 * kc + 1][0], pk[2 * kc + 1][1]));
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        // lane lr of group lq points at key (base + lr/4), dims 16db + 4*(lr%4) .. +3
-        const char* src0 = vs + (32 * kc + 4 * lq + lr / 4) * VROW + (16 * db + 4 * (lr % 4)) * 2;
-        const char* src1 = src0 + 16 * VROW;
+        // lane lr of group lq points at key (kgo + 32kc + 4lq + lr/4), dims 16db + 4*(lr%4) .. +3
+        const char* src0 = vs + (kgo + 32 * kc) * ROWB + v_rd(db);
         const i16x4 lo4 = lds_read_tr16(src0);
-        const i16x4 hi4 = lds_read_tr16(src1);
+        const i16x4 hi4 = lds_read_tr16(src0 + 16 * ROWB);
         const v8 av = __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
         mfma_t<TC>::run(av, bp, acc_o[db]);
       }
     }
   };
-  load_regs(lo, kreg, vreg);
-  for (int kt0 = lo; kt0 < hi; kt0 += kBN) tile_step(kt0, kreg, vreg);
 
+  bool stores_pending = false;  // cache stores of new tokens issued after the loads still counted on
+  // one tile: wait for its loads, free the oldest stage, refill it kStages - 1 tiles ahead, compute
+  auto step = [&](int t, auto st) __attribute__((always_inline)) {
+    constexpr int S = decltype(st)::value;
+    const int kt0 = lo + t * kBN;
+    // this wave's loads of tile t have landed: later tiles' loads (at most
+    // kStages - 2 of them, LPT operations each) may still be in flight
+    const int later = min(kStages - 2, ntiles - 1 - t);
+    if (stores_pending || later <= 0) {
+      wait_vmcnt<0>();
+      stores_pending = false;
+    } else if (later == 1) {
+      wait_vmcnt<LPT>();
+    } else {
+      wait_vmcnt<(kStages >= 4 ? 2 * LPT : LPT)>();
+    }
+    __syncthreads();  // every wave's loads of tile t landed; tile t - 1's stage is free
+    char* ks = stage_k(st);
+    char* vs = stage_v(st);
+    char* kme = ks + wave * NI * kWave * 16 + lane * 16;  // this lane's landed chunks (slot i at + i * 1 KiB)
+    char* vme = vs + wave * NI * kWave * 16 + lane * 16;
+    if (kt0 + kBN > hi || (LK == 2 && pages_bad)) {
+      // keys past the span (and outside the page pool) are zero, as if never loaded
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int j = kt0 + lrow(i);
+        bool zero = j >= hi;
+        if constexpr (LK == 2) zero = zero || (j < new_lo && cache_pos(j) < 0);
+        if (zero) {
+          *reinterpret_cast<uint4*>(kme + i * kWave * 16) = make_uint4(0, 0, 0, 0);
+          *reinterpret_cast<uint4*>(vme + i * kWave * 16) = make_uint4(0, 0, 0, 0);
+        }
+      }
+      __syncthreads();
+    }
+    if (kt0 + kBN > own_lo) {
+      // the tile holds new tokens this workgroup stores into the cache
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int j = kt0 + lrow(i);
+        const int64_t pj = (j >= own_lo && j < hi) ? (contiguous ? j : cache_pos(j)) : -1;
+        if (pj >= 0) {
+          *reinterpret_cast<uint4*>(const_cast<char*>(kbase) + pj * kst + lcol(i)) =
+              *reinterpret_cast<const uint4*>(kme + i * kWave * 16);
+          *reinterpret_cast<uint4*>(const_cast<char*>(vbase) + pj * vst + lcol(i)) =
+              *reinterpret_cast<const uint4*>(vme + i * kWave * 16);
+        }
+      }
+      stores_pending = true;
+    }
+    if (t + kStages - 1 < ntiles) issue(t + kStages - 1, std::integral_constant<int, (S + kStages - 1) % kStages>{});
+    compute(kt0, ks, vs);
+  };
+
+  if (ntiles > 0) issue(0, std::integral_constant<int, 0>{});
+  if (kStages >= 3 && ntiles > 1) issue(1, std::integral_constant<int, 1 % kStages>{});
+  if (kStages >= 4 && ntiles > 2) issue(2, std::integral_constant<int, 2 % kStages>{});
+  for (int t = 0; t < ntiles; t += kStages) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
+    if (kStages >= 3 && t + 2 < ntiles) step(t + 2, std::integral_constant<int, 2 % kStages>{});
+    if (kStages >= 4 && t + 3 < ntiles) step(t + 3, std::integral_constant<int, 3 % kStages>{});
+  }
+
+  if constexpr (kKeyGroups == 2) {
+    // ---- the second key group's (m, l, o) join the first's through LDS (the ring is free) ----
+    __syncthreads();
+    f4v* xo = reinterpret_cast<f4v*>(ring0[0]);          // [row wave][db][lane]: 32 KiB for D = 128
+    float2* xml = reinterpret_cast<float2*>(ring1[0]);   // [row wave][lane]
+    static_assert(kRowWaves * DB * kWave * 16 <= 2 * TILEB, "merge buffer");
+    if (kg == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db) xo[(rw * DB + db) * kWave + lane] = acc_o[db];
+      xml[rw * kWave + lane] = make_float2(m_run, l_run);
+    }
+    __syncthreads();
+    if (kg == 1) return;
+    const float2 ml1 = xml[rw * kWave + lane];
+    const float m_all = fmaxf(m_run, ml1.x);
+    const float a0 = fast_exp2(m_run - m_all), a1 = fast_exp2(ml1.x - m_all);
+    l_run = l_run * a0 + ml1.y * a1;
+    m_run = m_all;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) acc_o[db] = acc_o[db] * a0 + xo[(rw * DB + db) * kWave + lane] * a1;
+  }
   if (!row_ok) return;
   if (span.nsplit > 1) {
     // ---- partials for the merge kernel: o unnormalised, (m, l) once per row ----
@@ -497,23 +643,29 @@ __global__ __launch_bounds__(kChunkWaves * kWave) void chunk_attn_kernel(const C
   }
 }
 
-template <typename TC, int D, int LK>
-hipError_t launch_ci(const ChunkParams& p, int gb, hipStream_t stream) {
+template <typename TC, int D, int LK, int ROWS>
+hipError_t launch_cr(const ChunkParams& p, int gb, hipStream_t stream) {
   const int64_t n_wg = static_cast<int64_t>(kXcdsC) * p.n_qtiles * p.num_splits * ((p.n_groups + kXcdsC - 1) / kXcdsC);
   const dim3 grid(static_cast<unsigned>(n_wg)), block(kChunkWaves * kWave);
   switch (gb) {
-    case 8: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 8, LK>), grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 4, LK>), grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 2, LK>), grid, block, 0, stream, p); break;
-    default: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 1, LK>), grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 8, LK, ROWS>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 4, LK, ROWS>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 2, LK, ROWS>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((chunk_attn_kernel<TC, D, 1, LK, ROWS>), grid, block, 0, stream, p); break;
   }
   return hipGetLastError();
 }
 
+template <typename TC, int D, int LK>
+hipError_t launch_ci(const ChunkParams& p, int gb, int rows, hipStream_t stream) {
+  return rows == kChunkRowsLarge ? launch_cr<TC, D, LK, kChunkRowsLarge>(p, gb, stream)
+                                 : launch_cr<TC, D, LK, kChunkRowsSmall>(p, gb, stream);
+}
+
 template <typename TC, int D>
-hipError_t launch_c(const ChunkParams& p, int gb, hipStream_t stream) {
-  if (p.pages.table != nullptr) return launch_ci<TC, D, 2>(p, gb, stream);
-  return p.indirect ? launch_ci<TC, D, 1>(p, gb, stream) : launch_ci<TC, D, 0>(p, gb, stream);
+hipError_t launch_c(const ChunkParams& p, int gb, int rows, hipStream_t stream) {
+  if (p.pages.table != nullptr) return launch_ci<TC, D, 2>(p, gb, rows, stream);
+  return p.indirect ? launch_ci<TC, D, 1>(p, gb, rows, stream) : launch_ci<TC, D, 0>(p, gb, rows, stream);
 }
 
 }  // namespace
@@ -525,8 +677,6 @@ bool chunk_supports(const nc_attn_args& a) {
          (a.cache_dtype == NC_DTYPE_BF16 || a.cache_dtype == NC_DTYPE_F16) &&
          (a.head_dim == 64 || a.head_dim == 128) && tile_bytes < (int64_t(1) << 31);
 }
-
-int chunk_rows_per_wg() { return kRows; }
 
 hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream,
                         const RowFilter* rows) {
@@ -554,7 +704,7 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.n_kv_heads = static_cast<int32_t>(a.n_kv_heads);
   p.group = plan.group;
   p.n_hblocks = plan.n_hblocks;
-  const int qb = kRows / plan.head_block;
+  const int qb = plan.chunk_rows / plan.head_block;
   p.n_qtiles = static_cast<int32_t>((a.t_new + qb - 1) / qb);
   p.n_groups = a.batch * a.n_kv_heads * plan.n_hblocks;
   p.window = a.window_left;
@@ -573,12 +723,13 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
   p.v_sb = a.v_stride_b; p.v_st = a.v_stride_t; p.v_sh = a.v_stride_h;
   p.err = a.error_flag;
+  const int wg_rows = plan.chunk_rows;
   if (a.cache_dtype == NC_DTYPE_BF16) {
-    return a.head_dim == 64 ? launch_c<bf16, 64>(p, plan.head_block, stream)
-                            : launch_c<bf16, 128>(p, plan.head_block, stream);
+    return a.head_dim == 64 ? launch_c<bf16, 64>(p, plan.head_block, wg_rows, stream)
+                            : launch_c<bf16, 128>(p, plan.head_block, wg_rows, stream);
   }
-  return a.head_dim == 64 ? launch_c<f16, 64>(p, plan.head_block, stream)
-                          : launch_c<f16, 128>(p, plan.head_block, stream);
+  return a.head_dim == 64 ? launch_c<f16, 64>(p, plan.head_block, wg_rows, stream)
+                          : launch_c<f16, 128>(p, plan.head_block, wg_rows, stream);
 }
 
 }  // namespace nckv

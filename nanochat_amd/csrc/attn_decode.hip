@@ -107,7 +107,7 @@ hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const
   p.tickets = nullptr;
   p.num_splits = plan.chunk_splits;
   p.keys_per_split = plan.chunk_keys_per_split;
-  p.merge_qb = chunk_rows_per_wg() / plan.head_block;
+  p.merge_qb = plan.chunk_rows / plan.head_block;
   set_divisors(p);
   switch (a.head_dim) {
     case 32: return launch_merge_d<32>(p, plan.head_block, stream);

@@ -90,6 +90,8 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   if (!valid_dtype(a.q_dtype) || !valid_dtype(a.cache_dtype)) return NC_ERR_DTYPE;
   if (!decode_supports(a.cache_dtype, a.head_dim)) return NC_ERR_HEAD_DIM;
   if (a.keys_per_split < 0 || a.keys_per_split % 64 != 0) return NC_ERR_BAD_SHAPE;
+  // the kernels take running maxima of unscaled scores: the scale must be positive (and finite)
+  if (!(a.softmax_scale > 0.0f) || !(a.softmax_scale < 3.0e38f)) return NC_ERR_BAD_SHAPE;
   if (a.cache_batch_idx != nullptr && a.cache_batch <= 0) return NC_ERR_BAD_SHAPE;
   if (a.cu_seqlens_q != nullptr && (a.total_q < 0 || a.total_q > INT32_MAX)) return NC_ERR_BAD_SHAPE;
   if (!valid_pages(a.page_table, a.page_table_stride, a.page_size, a.num_blocks, a.t_max, a.cache_batch_idx,
@@ -146,9 +148,13 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   plan->use_chunk = a.t_new >= kChunkMinTokens && chunk_supports(a);
   plan->chunk_keys_per_split = 0;
   plan->chunk_splits = 1;
+  plan->chunk_rows = kChunkRowsSmall;
   if (plan->use_chunk) {
+    const int64_t units = (a.t_new + kChunkRowsSmall / hb - 1) / (kChunkRowsSmall / hb) * a.batch * a.n_kv_heads *
+                          plan->n_hblocks;
+    if (units >= kChunkLargeAt) plan->chunk_rows = kChunkRowsLarge;
     // one workgroup's keys span at most (window + its queries) or the cache length
-    const int64_t qb = chunk_rows_per_wg() / hb;
+    const int64_t qb = plan->chunk_rows / hb;
     const int64_t span = a.window_left >= 0 ? std::min<int64_t>(a.t_max, int64_t(a.window_left) + qb) : a.t_max;
     int64_t ckps = a.keys_per_split;
     if (ckps == 0) {

@@ -39,6 +39,7 @@ struct AttnPlan {
   bool wide;           // decode with 8-wave workgroups and one split (few groups, short rows)
   bool merge_in_kernel;  // decode splits merged by their last workgroup (tickets), no merge launch
   bool use_chunk;      // T_new > 1 on the MFMA chunk kernel
+  int chunk_rows;      // (query, head) rows per chunk workgroup: kChunkRowsSmall or kChunkRowsLarge
   int chunk_keys_per_split;
   int chunk_splits;    // > 1: chunk partials merged by the split-merge kernel
   // varlen batch on the chunk kernel: its single-token rows run on the decode
@@ -73,7 +74,15 @@ bool decode_wide_supported(int head_block, int64_t head_dim);
 bool chunk_supports(const nc_attn_args& a);
 hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream,
                         const RowFilter* rows = nullptr);
-int chunk_rows_per_wg();
+// Chunk workgroups own 64 (query, head) rows (two wave groups share each key
+// tile) while the call has fewer than kChunkLargeAt (q tile, kv head, head
+// block) units at 64 rows, and 128 rows (each key tile feeds twice the rows)
+// from there on.  Measured on MI355X (ms): d24 1024-token prefill (192 units)
+// 0.54 at 64 rows, 0.75 at 128; C5's 16 chunk rows (512 units) 4.39 at 64
+// rows, 4.01 at 128.
+constexpr int kChunkRowsSmall = 64;
+constexpr int kChunkRowsLarge = 128;
+constexpr int64_t kChunkLargeAt = 512;
 // Split merge of the chunk kernel's partials (plan.chunk_splits > 1).
 hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
                               hipStream_t stream, const RowFilter* rows = nullptr);
