@@ -643,6 +643,100 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
   }
 }
 
+// Split merge of the chunk kernel's partials: block (group, q tile, 64-row
+// slice) combines the slots of the slice's 64 (query, head) rows with the
+// log-sum-exp rule.  A chunk workgroup's key span, hence its split count, is
+// the same for all its rows, so a block whose tile ran unsplit returns after
+// one read of cache_seqlens.  Four threads per row, each folding D / 4
+// consecutive dims over the splits, kMergeCH splits per memory round trip.
+constexpr int kMergeCH = 4;
+
+template <typename TC, int D, int GB, int ROWS, bool IND>
+__global__ __launch_bounds__(256) void chunk_merge_kernel(const ChunkParams p) {
+  constexpr int QB = ROWS / GB;
+  constexpr int SLICES = ROWS / 64;
+  constexpr int DT = D / 4;               // dims per thread
+  const uint32_t pb = blockIdx.x;
+  const int slice = static_cast<int>(pb % SLICES);
+  uint32_t rem;
+  const uint32_t gt = pb / SLICES;
+  const uint32_t gq = fdivmod(gt, p.fd_qtiles, rem);
+  const int qt = static_cast<int>(rem);
+  uint32_t group = gq;
+  if (group >= p.n_groups) return;
+  const int hb = static_cast<int>(group % static_cast<uint32_t>(p.n_hblocks));
+  group /= static_cast<uint32_t>(p.n_hblocks);
+  const int hk = static_cast<int>(group % static_cast<uint32_t>(p.n_kv_heads));
+  const int64_t b = group / static_cast<uint32_t>(p.n_kv_heads);
+  RowQ rq{b * p.t_new, p.t_new};
+  if constexpr (IND) {
+    if (cache_row(p.cache_idx, p.cache_batch, b, nullptr, false) < 0) return;  // the row was skipped
+    rq = row_queries(p.cu_q, p.total_q, b, p.q_bound, nullptr, false);
+    if (rq.len < p.len_lo || rq.len > p.len_hi) return;  // another launch's row (or skipped)
+  }
+  const int q0 = qt * QB;
+  if (q0 >= rq.len) return;
+  const int q_end = min(q0 + QB, rq.len);
+  const int nsplit = chunk_span(p.seqlens[b], q0, q_end, p.t_max, p.window, p.keys_per_split).nsplit;
+  if (nsplit <= 1) return;  // the chunk workgroup wrote these outputs itself
+  const int row = slice * 64 + static_cast<int>(threadIdx.x) / 4;
+  const int qi = q0 + row / GB;
+  if (qi >= rq.len) return;
+  const int h = hk * p.group + hb * GB + row % GB;
+  const int d0 = (threadIdx.x % 4) * DT;
+  const int64_t pair_row = (b * p.t_new + qi) * p.n_heads + h;
+  const float* ml = p.part_ml + pair_row * p.num_splits * 2;
+  const float* po = p.part_o + pair_row * p.num_splits * D + d0;
+  float M = kNegBigC, L = 0.0f, O[DT];
+#pragma unroll
+  for (int e = 0; e < DT; ++e) O[e] = 0.0f;
+  for (int sp0 = 0; sp0 < nsplit; sp0 += kMergeCH) {
+    float ms[kMergeCH], ls[kMergeCH];
+    float4 os[kMergeCH][DT / 4];
+#pragma unroll
+    for (int u = 0; u < kMergeCH; ++u) {
+      const int sp = sp0 + u;
+      const bool in = sp < nsplit;
+      const float2 v = in ? *reinterpret_cast<const float2*>(ml + 2 * sp) : make_float2(kNegBigC, 0.0f);
+      ms[u] = v.x;
+      ls[u] = v.y;
+#pragma unroll
+      for (int e = 0; e < DT / 4; ++e) {
+        os[u][e] = in ? *reinterpret_cast<const float4*>(po + static_cast<int64_t>(sp) * D + 4 * e)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float mx = M;
+#pragma unroll
+    for (int u = 0; u < kMergeCH; ++u) mx = ls[u] > 0.0f ? fmaxf(mx, ms[u]) : mx;
+    const float a = fast_exp2(M - mx);
+    L *= a;
+#pragma unroll
+    for (int e = 0; e < DT; ++e) O[e] *= a;
+#pragma unroll
+    for (int u = 0; u < kMergeCH; ++u) {
+      const bool live = ls[u] > 0.0f;  // l == 0: every key of the split masked for this row
+      const float w = live ? fast_exp2(ms[u] - mx) : 0.0f;
+      L = __builtin_fmaf(ls[u], w, L);
+#pragma unroll
+      for (int e = 0; e < DT / 4; ++e) {
+        O[4 * e + 0] = live ? __builtin_fmaf(os[u][e].x, w, O[4 * e + 0]) : O[4 * e + 0];
+        O[4 * e + 1] = live ? __builtin_fmaf(os[u][e].y, w, O[4 * e + 1]) : O[4 * e + 1];
+        O[4 * e + 2] = live ? __builtin_fmaf(os[u][e].z, w, O[4 * e + 2]) : O[4 * e + 2];
+        O[4 * e + 3] = live ? __builtin_fmaf(os[u][e].w, w, O[4 * e + 3]) : O[4 * e + 3];
+      }
+    }
+    M = mx;
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  uint16_t* op = reinterpret_cast<uint16_t*>(p.out) + ((rq.tok0 + qi) * p.n_heads + h) * static_cast<int64_t>(D) + d0;
+#pragma unroll
+  for (int e = 0; e < DT; e += 2) {
+    const uint32_t w = mfma_t<TC>::pack2(O[e] * inv, O[e + 1] * inv);
+    *reinterpret_cast<uint32_t*>(op + e) = w;
+  }
+}
+
 template <typename TC, int D, int LK, int ROWS>
 hipError_t launch_cr(const ChunkParams& p, int gb, hipStream_t stream) {
   const int64_t n_wg = static_cast<int64_t>(kXcdsC) * p.n_qtiles * p.num_splits * ((p.n_groups + kXcdsC - 1) / kXcdsC);
@@ -668,18 +762,31 @@ hipError_t launch_c(const ChunkParams& p, int gb, int rows, hipStream_t stream) 
   return p.indirect ? launch_ci<TC, D, 1>(p, gb, rows, stream) : launch_ci<TC, D, 0>(p, gb, rows, stream);
 }
 
-}  // namespace
-
-bool chunk_supports(const nc_attn_args& a) {
-  // a key tile's byte span (64 cache rows) must fit the kernel's 32-bit offsets
-  const int64_t tile_bytes = kBN * std::max(std::abs(a.kc_stride_t), std::abs(a.vc_stride_t)) * 2;
-  return a.t_new > 1 && a.q_dtype == a.cache_dtype &&
-         (a.cache_dtype == NC_DTYPE_BF16 || a.cache_dtype == NC_DTYPE_F16) &&
-         (a.head_dim == 64 || a.head_dim == 128) && tile_bytes < (int64_t(1) << 31);
+template <typename TC, int D, bool IND, int ROWS>
+hipError_t launch_merge_cr(const ChunkParams& p, int gb, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(p.n_groups * p.n_qtiles * (ROWS / 64))), block(256);
+  switch (gb) {
+    case 8: hipLaunchKernelGGL((chunk_merge_kernel<TC, D, 8, ROWS, IND>), grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL((chunk_merge_kernel<TC, D, 4, ROWS, IND>), grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL((chunk_merge_kernel<TC, D, 2, ROWS, IND>), grid, block, 0, stream, p); break;
+    default: hipLaunchKernelGGL((chunk_merge_kernel<TC, D, 1, ROWS, IND>), grid, block, 0, stream, p); break;
+  }
+  return hipGetLastError();
 }
 
-hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream,
-                        const RowFilter* rows) {
+template <typename TC, int D>
+hipError_t launch_merge_c(const ChunkParams& p, int gb, int rows, hipStream_t stream) {
+  if (p.indirect) {
+    return rows == kChunkRowsLarge ? launch_merge_cr<TC, D, true, kChunkRowsLarge>(p, gb, stream)
+                                   : launch_merge_cr<TC, D, true, kChunkRowsSmall>(p, gb, stream);
+  }
+  return rows == kChunkRowsLarge ? launch_merge_cr<TC, D, false, kChunkRowsLarge>(p, gb, stream)
+                                 : launch_merge_cr<TC, D, false, kChunkRowsSmall>(p, gb, stream);
+}
+
+// Launch parameters of a chunk call (and of its split merge).
+ChunkParams make_chunk_params(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
+                              const RowFilter* rows) {
   ChunkParams p;
   p.q = a.q; p.out = a.out;
   p.kc = static_cast<const char*>(a.k_cache); p.vc = static_cast<const char*>(a.v_cache);
@@ -723,6 +830,22 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   p.k_sb = a.k_stride_b; p.k_st = a.k_stride_t; p.k_sh = a.k_stride_h;
   p.v_sb = a.v_stride_b; p.v_st = a.v_stride_t; p.v_sh = a.v_stride_h;
   p.err = a.error_flag;
+  return p;
+}
+
+}  // namespace
+
+bool chunk_supports(const nc_attn_args& a) {
+  // a key tile's byte span (64 cache rows) must fit the kernel's 32-bit offsets
+  const int64_t tile_bytes = kBN * std::max(std::abs(a.kc_stride_t), std::abs(a.vc_stride_t)) * 2;
+  return a.t_new > 1 && a.q_dtype == a.cache_dtype &&
+         (a.cache_dtype == NC_DTYPE_BF16 || a.cache_dtype == NC_DTYPE_F16) &&
+         (a.head_dim == 64 || a.head_dim == 128) && tile_bytes < (int64_t(1) << 31);
+}
+
+hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, hipStream_t stream,
+                        const RowFilter* rows) {
+  const ChunkParams p = make_chunk_params(a, plan, s, rows);
   const int wg_rows = plan.chunk_rows;
   if (a.cache_dtype == NC_DTYPE_BF16) {
     return a.head_dim == 64 ? launch_c<bf16, 64>(p, plan.head_block, wg_rows, stream)
@@ -730,6 +853,18 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
   }
   return a.head_dim == 64 ? launch_c<f16, 64>(p, plan.head_block, wg_rows, stream)
                           : launch_c<f16, 128>(p, plan.head_block, wg_rows, stream);
+}
+
+hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
+                              hipStream_t stream, const RowFilter* rows) {
+  const ChunkParams p = make_chunk_params(a, plan, s, rows);
+  const int wg_rows = plan.chunk_rows;
+  if (a.cache_dtype == NC_DTYPE_BF16) {
+    return a.head_dim == 64 ? launch_merge_c<bf16, 64>(p, plan.head_block, wg_rows, stream)
+                            : launch_merge_c<bf16, 128>(p, plan.head_block, wg_rows, stream);
+  }
+  return a.head_dim == 64 ? launch_merge_c<f16, 64>(p, plan.head_block, wg_rows, stream)
+                          : launch_merge_c<f16, 128>(p, plan.head_block, wg_rows, stream);
 }
 
 }  // namespace nckv

@@ -35,7 +35,6 @@ void set_divisors(DecodeParams& p) {
   p.fd_t_new = make_fastdiv(static_cast<uint32_t>(p.t_new));
   p.fd_splits = make_fastdiv(static_cast<uint32_t>(p.num_splits));
   p.fd_kps = make_fastdiv(static_cast<uint32_t>(p.keys_per_split));
-  p.fd_qb = make_fastdiv(static_cast<uint32_t>(p.merge_qb > 0 ? p.merge_qb : 1));
 }
 
 DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s, bool fused_append) {
@@ -71,7 +70,6 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.num_splits = plan.num_splits;
   p.keys_per_split = plan.keys_per_split;
   p.fused = fused_append ? 1 : 0;
-  p.merge_qb = 0;
   p.rope_cos = p.rope_sin = nullptr;
   p.rope = 0;
   p.rope_len = 1;
@@ -83,39 +81,7 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   return p;
 }
 
-template <int D>
-hipError_t launch_merge_d(const DecodeParams& p, int gb, hipStream_t stream) {
-  switch (gb) {
-    case 8: launch_merge_g<D, 8>(p, stream); break;
-    case 4: launch_merge_g<D, 4>(p, stream); break;
-    case 2: launch_merge_g<D, 2>(p, stream); break;
-    default: launch_merge_g<D, 1>(p, stream); break;
-  }
-  return hipGetLastError();
-}
-
 }  // namespace
-
-hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
-                              hipStream_t stream, const RowFilter* rows) {
-  DecodeParams p = make_params(a, plan, s, false);
-  if (rows != nullptr) {
-    p.len_lo = rows->lo;
-    p.len_hi = rows->hi;
-    p.q_bound = rows->bound;
-  }
-  p.tickets = nullptr;
-  p.num_splits = plan.chunk_splits;
-  p.keys_per_split = plan.chunk_keys_per_split;
-  p.merge_qb = plan.chunk_rows / plan.head_block;
-  set_divisors(p);
-  switch (a.head_dim) {
-    case 32: return launch_merge_d<32>(p, plan.head_block, stream);
-    case 64: return launch_merge_d<64>(p, plan.head_block, stream);
-    case 128: return launch_merge_d<128>(p, plan.head_block, stream);
-    default: return launch_merge_d<256>(p, plan.head_block, stream);
-  }
-}
 
 hipError_t launch_decode(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
                          bool fused_append, const nc_qk_prologue* prologue, hipStream_t stream,

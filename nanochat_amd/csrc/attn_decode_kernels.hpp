@@ -30,9 +30,10 @@
 //    release/acquire fences, buffer_wbl2 / buffer_inv, which measured 3-10x
 //    slower on MI355X) and no waiting on other workgroups: the last arrival
 //    finds every partial complete.
-//  - merge_splits_kernel, the next launch on the stream (chunk splits, and
-//    decode plans with more groups than tickets): it recomputes the query's
-//    split count from cache_seqlens and combines exactly those slots.
+//  - merge_splits_kernel, the next launch on the stream (decode plans with
+//    more groups or workgroups than the in-kernel merge takes): it recomputes
+//    the query's split count from cache_seqlens and combines exactly those
+//    slots.  (The chunk kernel's splits have a merge kernel of their own.)
 // The splits of one (b, t, unit) run on one XCD (workgroups are dispatched
 // round-robin over the 8 XCDs), next to each other in launch order.
 //
@@ -109,14 +110,13 @@ struct DecodeParams {
   int32_t q_dtype;
   int32_t num_splits, keys_per_split;
   int32_t fused;
-  int32_t merge_qb;  // split merge: 0 = decode splits (per query); > 0 = chunk splits (per QB-query tile)
   // fused QK prologue (rotary, RMS norm, scale) on q and the appended k; rope == 0: off
   const void* rope_cos;
   const void* rope_sin;
   int32_t rope, rope_len, rope_dtype, rope_half;  // rope_half = head_dim / 2 (table row length)
   float rope_scale, rope_eps;
   // divisors of the block-index decompositions (every index is < 2^31: the plan caps the grid)
-  FastDiv fd_hblocks, fd_kv_heads, fd_t_new, fd_splits, fd_kps, fd_qb;
+  FastDiv fd_hblocks, fd_kv_heads, fd_t_new, fd_splits, fd_kps;
 };
 
 namespace {
@@ -248,17 +248,17 @@ template <> struct MergeVec<4> {
   }
 };
 
-// Second pass: block g combines the split partials of group g's GB heads.
-// The block recomputes how many splits its query's producer used (decode:
-// the query's key range; chunk: its workgroup's span) and reads exactly those
-// slots; a query with one split was written directly by its producer.  Each
+// Second pass of the decode splits: block g combines the split partials of
+// group g's GB heads.  The block recomputes how many splits its query's
+// producer used (from the query's key range) and reads exactly those slots;
+// a query with one split was written directly by its producer.  Each
 // thread owns VE consecutive output elements of one head and folds the slots
 // in chunks of CH with every load of a chunk in flight together ((m, l) reads
 // are uniform per head), so up to CH splits cost one memory round trip.  The
 // number of dependent round trips, not the bytes, sets this kernel's time;
 // two shapes are instantiated: <CH 16, VE 1> (few VGPRs, high occupancy: many
-// merge blocks, few splits) and <CH 32, VE 4> (decode with more than 16
-// splits: one or two round trips for up to 64 splits).  Slots with l == 0
+// merge blocks, few splits) and <CH 32, VE 4> (more than 16 splits: one or
+// two round trips for up to 64 splits).  Slots with l == 0
 // (every key of the split masked for this query) contribute nothing.
 // IND: the launch passes cache_batch_idx or cu_seqlens_q (per-row lookups).
 // Plain launches use IND = false kernels, which hold no lookup code at all:
@@ -275,18 +275,11 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
     // no such query in this row, the row is another launch's, or it was skipped
     if (rq.len < p.len_lo || rq.len > p.len_hi || gi.t >= rq.len) return;
   }
-  int nsplit;
-  if (p.merge_qb == 0) {
-    nsplit = key_range(p, gi.b, gi.t).nsplit;
-  } else {
-    const int q0 = static_cast<int>(fdiv(static_cast<uint32_t>(gi.t), p.fd_qb)) * p.merge_qb;
-    nsplit = chunk_span(p.seqlens[gi.b], q0, min(q0 + p.merge_qb, rq.len), p.t_max, p.window,
-                        p.keys_per_split).nsplit;
-  }
-  // Decode splits with at most CH slots: load every allocated slot without
-  // waiting for cache_seqlens (one memory round trip instead of two); slots
-  // past the query's split count hold stale data and are masked out below.
-  const bool eager = p.merge_qb == 0 && p.num_splits <= CH;
+  const int nsplit = key_range(p, gi.b, gi.t).nsplit;
+  // At most CH slots: load every allocated slot without waiting for
+  // cache_seqlens (one memory round trip instead of two); slots past the
+  // query's split count hold stale data and are masked out below.
+  const bool eager = p.num_splits <= CH;
   if (!eager && nsplit <= 1) return;
   const int lim = eager ? p.num_splits : nsplit;
   const int64_t pair0 = (gi.b * p.t_new + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;
@@ -349,7 +342,7 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
 template <int D, int GB, bool IND>
 void launch_merge_i(const DecodeParams& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.n_groups));
-  if (p.merge_qb == 0 && p.num_splits > 16) {
+  if (p.num_splits > 16) {
     hipLaunchKernelGGL((merge_splits_kernel<D, GB, 32, 4, IND>), grid, dim3(merge_threads(D, GB, 4)), 0, stream, p);
   } else {
     hipLaunchKernelGGL((merge_splits_kernel<D, GB, 16, 1, IND>), grid, dim3(merge_threads(D, GB, 1)), 0, stream, p);

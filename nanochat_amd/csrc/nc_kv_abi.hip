@@ -160,7 +160,10 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
     if (ckps == 0) {
       // workgroups of one row per split: q tiles x kv heads x head blocks
       const int64_t per_row = (a.t_new + qb - 1) / qb * a.n_kv_heads * plan->n_hblocks;
-      const int64_t want = (span * per_row + kChunkWGPerRow - 1) / kChunkWGPerRow;
+      // 128-row workgroups aim at half as many per row (C5's chunk rows: 2048-key splits, 3.93 vs
+      // 4.02 ms/step at 1024; fewer partials for the merge)
+      const int64_t wg_per_row = kChunkWGPerRow * kChunkRowsSmall / plan->chunk_rows;
+      const int64_t want = (span * per_row + wg_per_row - 1) / wg_per_row;
       ckps = span > kChunkSplitAbove
                  ? std::min(span, std::max(kChunkSplitUnit, (want + kChunkSplitUnit - 1) / kChunkSplitUnit * kChunkSplitUnit))
                  : span;
