@@ -255,18 +255,23 @@ template <> struct MergeVec<4> {
 // thread owns VE consecutive output elements of one head and folds the slots
 // in chunks of CH with every load of a chunk in flight together ((m, l) reads
 // are uniform per head), so up to CH splits cost one memory round trip.  The
-// number of dependent round trips, not the bytes, sets this kernel's time;
-// two shapes are instantiated: <CH 16, VE 1> (few VGPRs, high occupancy: many
-// merge blocks, few splits) and <CH 32, VE 4> (more than 16 splits: one or
-// two round trips for up to 64 splits).  Slots with l == 0
-// (every key of the split masked for this query) contribute nothing.
+// number of dependent round trips, not the bytes, sets this kernel's time:
+// EAGER kernels (the plan's split count is at most CH) load every allocated
+// slot right after the kernel arguments, without waiting for cache_seqlens,
+// and mask the slots past the query's split count afterwards.  Shapes:
+// <CH 16, VE 1> (few VGPRs, high occupancy: many merge blocks, few splits)
+// and <CH 32, VE 4> (more than 16 splits: one or two round trips for up to
+// 64 splits).  Slots with l == 0 (every key of the split masked for this
+// query) contribute nothing.
 // IND: the launch passes cache_batch_idx or cu_seqlens_q (per-row lookups).
 // Plain launches use IND = false kernels, which hold no lookup code at all:
 // its mere presence, never executed, measured 3% slower on the C5 batch.
-template <int D, int GB, int CH, int VE, bool IND>
+template <int D, int GB, int CH, int VE, bool IND, bool EAGER>
 __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p) {
   typedef typename MergeVec<VE>::T VT;
   constexpr int TPH = D / VE;  // threads per head
+  pin_args(p.fd_hblocks, p.fd_kv_heads, p.fd_t_new, p.fd_kps, p.seqlens, p.part_ml, p.part_o, p.out,
+           p.num_splits, p.keys_per_split, p.t_new, p.t_max, p.window, p.n_heads, p.group, p.q_dtype);
   const GroupIdx gi = group_index(p, blockIdx.x);
   RowQ rq{gi.b * p.t_new, p.t_new};
   if constexpr (IND) {
@@ -275,13 +280,12 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
     // no such query in this row, the row is another launch's, or it was skipped
     if (rq.len < p.len_lo || rq.len > p.len_hi || gi.t >= rq.len) return;
   }
-  const int nsplit = key_range(p, gi.b, gi.t).nsplit;
-  // At most CH slots: load every allocated slot without waiting for
-  // cache_seqlens (one memory round trip instead of two); slots past the
-  // query's split count hold stale data and are masked out below.
-  const bool eager = p.num_splits <= CH;
-  if (!eager && nsplit <= 1) return;
-  const int lim = eager ? p.num_splits : nsplit;
+  int nsplit = 0;
+  if constexpr (!EAGER) {
+    nsplit = key_range(p, gi.b, gi.t).nsplit;
+    if (nsplit <= 1) return;
+  }
+  const int lim = EAGER ? p.num_splits : nsplit;
   const int64_t pair0 = (gi.b * p.t_new + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;
   const int64_t opair0 = (rq.tok0 + gi.t) * p.n_heads + gi.hk * p.group + gi.hb * GB;  // row of `out`
   for (int e = threadIdx.x; e < GB * TPH; e += blockDim.x) {
@@ -294,23 +298,24 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
     for (int sp0 = 0; sp0 < lim; sp0 += CH) {
       float ms[CH], ls[CH];
       VT os[CH];
+      // Slot indices past `lim` are clamped to the last allocated slot (an
+      // in-bounds duplicate, masked below) rather than branched around: a
+      // branch per slot made the compiler wait for each load before issuing
+      // the next (one round trip per slot).
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
-        const int sp = sp0 + u;
-        if (sp < lim) {
-          const float2 v = *reinterpret_cast<const float2*>(ml + 2 * sp);
-          ms[u] = v.x;
-          ls[u] = v.y;
-          os[u] = *reinterpret_cast<const VT*>(po + static_cast<int64_t>(sp) * D);
-        } else {
-          ms[u] = kNegBig;
-          ls[u] = 0.0f;
-          os[u] = VT{};
-        }
+        const int sp = min(sp0 + u, lim - 1);
+        const float2 v = *reinterpret_cast<const float2*>(ml + 2 * sp);
+        ms[u] = v.x;
+        ls[u] = v.y;
+        os[u] = *reinterpret_cast<const VT*>(po + static_cast<int64_t>(sp) * D);
       }
+      __builtin_amdgcn_sched_barrier(0);  // no use of a slot scheduled between the loads
+      // eager: the query's split count, read while the slot loads are in flight
+      if constexpr (EAGER) nsplit = key_range(p, gi.b, gi.t).nsplit;
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
-        if (sp0 + u >= nsplit) ls[u] = 0.0f;  // slot not written by this call
+        if (sp0 + u >= nsplit) ls[u] = 0.0f;  // slot not written by this call, or a clamped duplicate
       }
       float mx = M;
 #pragma unroll
@@ -342,10 +347,15 @@ __global__ __launch_bounds__(256) void merge_splits_kernel(const DecodeParams p)
 template <int D, int GB, bool IND>
 void launch_merge_i(const DecodeParams& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.n_groups));
-  if (p.num_splits > 16) {
-    hipLaunchKernelGGL((merge_splits_kernel<D, GB, 32, 4, IND>), grid, dim3(merge_threads(D, GB, 4)), 0, stream, p);
+  if (p.num_splits > 32) {
+    hipLaunchKernelGGL((merge_splits_kernel<D, GB, 32, 4, IND, false>), grid, dim3(merge_threads(D, GB, 4)), 0,
+                       stream, p);
+  } else if (p.num_splits > 16) {
+    hipLaunchKernelGGL((merge_splits_kernel<D, GB, 32, 4, IND, true>), grid, dim3(merge_threads(D, GB, 4)), 0,
+                       stream, p);
   } else {
-    hipLaunchKernelGGL((merge_splits_kernel<D, GB, 16, 1, IND>), grid, dim3(merge_threads(D, GB, 1)), 0, stream, p);
+    hipLaunchKernelGGL((merge_splits_kernel<D, GB, 16, 1, IND, true>), grid, dim3(merge_threads(D, GB, 1)), 0,
+                       stream, p);
   }
 }
 
@@ -403,6 +413,12 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int row = lane / LPK;
   const int col = lane % LPK;
+
+  // the arguments on the path to the first K/V load, in one batch (head
+  // blocks of 4 or 8 q heads: measured 2% slower, their loads already batch)
+  if constexpr (GB < 4) pin_args(p.fd_splits, p.n_groups, p.fd_hblocks, p.fd_kv_heads, p.fd_t_new, p.fd_kps, p.seqlens, p.t_max,
+           p.window, p.keys_per_split, p.num_splits, p.t_new, p.n_heads, p.group, p.fused, p.kc, p.vc, p.kc_sb,
+           p.kc_sh, p.kc_st, p.vc_sb, p.vc_sh, p.vc_st);
 
   // ---- block -> (group, split) ----
 #if NC_DECODE_XCD_MAP
@@ -799,11 +815,16 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
       float ms[kInKernelMergeChunk], ls[kInKernelMergeChunk], os[kInKernelMergeChunk];
 #pragma unroll
       for (int u = 0; u < kInKernelMergeChunk; ++u) {
-        const int sp = sp0 + u;
-        const bool in = sp < nsplit;
-        ms[u] = in ? coherent_load(ml + 2 * sp) : kNegBig;
-        ls[u] = in ? coherent_load(ml + 2 * sp + 1) : 0.0f;
-        os[u] = in ? coherent_load(po + static_cast<int64_t>(sp) * D) : 0.0f;
+        // clamped, not branched: every load of the chunk in flight together
+        const int sp = min(sp0 + u, nsplit - 1);
+        ms[u] = coherent_load(ml + 2 * sp);
+        ls[u] = coherent_load(ml + 2 * sp + 1);
+        os[u] = coherent_load(po + static_cast<int64_t>(sp) * D);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < kInKernelMergeChunk; ++u) {
+        if (sp0 + u >= nsplit) ls[u] = 0.0f;  // a clamped duplicate
       }
       float mx = M;
 #pragma unroll

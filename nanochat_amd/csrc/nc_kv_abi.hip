@@ -38,7 +38,10 @@ constexpr int64_t kDecodeGridTarget = NC_DECODE_GRID_TARGET;
 // Decode with wide workgroups and no split: at most this many groups (one per
 // CU) and this many keys per row.
 constexpr int64_t kWideMinGroups = 128;
-constexpr int64_t kWideMaxGroups = 256;
+#ifndef NC_DECODE_WIDE_MAX_GROUPS
+#define NC_DECODE_WIDE_MAX_GROUPS 256
+#endif
+constexpr int64_t kWideMaxGroups = NC_DECODE_WIDE_MAX_GROUPS;
 constexpr int64_t kWideMaxKeys = 4096;
 // Decode splits merged by their last workgroup (one uint32 ticket per group at
 // the start of every non-empty workspace) instead of a merge launch, for grids

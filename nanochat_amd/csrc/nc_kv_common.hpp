@@ -292,6 +292,27 @@ __device__ __forceinline__ uint32_t fdivmod(uint32_t n, const FastDiv& f, uint32
   return q;
 }
 
+// Kernel arguments in scalar registers from this point on.  The compiler
+// loads each argument next to its first use, after whatever early-exit
+// branches come before it, so a kernel prologue otherwise waits on one
+// scalar-cache round trip per branch (4-6 before the first vector load on the
+// decode kernels).  Naming the prologue's arguments here, before any branch,
+// issues all their loads as one batch.
+__device__ __forceinline__ void pin_arg(int32_t v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void pin_arg(uint32_t v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void pin_arg(int64_t v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void pin_arg(float v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void pin_arg(const void* v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void pin_arg(const FastDiv& f) {
+  pin_arg(f.d);
+  pin_arg(f.m);
+  pin_arg(f.l);
+}
+template <typename... T>
+__device__ __forceinline__ void pin_args(const T&... v) {
+  (pin_arg(v), ...);
+}
+
 // Key span [lo, hi) of the chunk-kernel workgroup that owns queries
 // [q0, q_end) of a row whose cache held s tokens, and its split count (>= 1;
 // an empty span is one split).  The chunk kernel and the split merge both use
