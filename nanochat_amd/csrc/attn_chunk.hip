@@ -91,14 +91,54 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((lds_char*)(p)));
 }
 
-typedef __attribute__((address_space(1))) const void global_cvoid;
-typedef __attribute__((address_space(3))) void lds_void;
 
 // One wave's 16-byte direct load into LDS (global_load_lds_dwordx4): lane l's
 // 16 bytes from `src` land at dst + 16 * l.  `dst` must be wave-uniform.  The
 // load counts in the wave's vector-memory counter like any other load.
+//
+// Issued as inline asm, so the compiler does not track it: with the builtin,
+// the compiler put an s_waitcnt vmcnt(0) before the transposed V reads
+// (ds_read_b64_tr_b16 carries no alias information), a wait for the next
+// tile's prefetch issued just before, which serialised every tile's load
+// latency with its compute.  The kernel's own counted waits (wait_vmcnt
+// before the barrier of each step) are what order a stage's loads before its
+// reads; the compiler's waits for its own vector loads stay conservative,
+// since loads complete in order and these only add younger ones.
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char*)(p)));
+}
+// m0 (the LDS base of the load) is a reserved register: nothing else in these
+// kernels reads it (LDS instructions do not use m0 on gfx9 and later), so
+// clobbering it here is safe and the compiler's warning about it is silenced.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const char* src, char* dst) {
-  __builtin_amdgcn_global_load_lds((global_cvoid*)src, (lds_void*)((lds_char*)dst), 16, 0, 0);
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_addr(dst))
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Reductions over the four lanes l, l ^ 16, l ^ 32, l ^ 48 (one query row's
+// lane groups) with the gfx950 lane-half swaps v_permlane16_swap (rows of 16
+// lanes: odd rows of the first operand with even rows of the second) and
+// v_permlane32_swap (upper 32 lanes with lower 32): swapping x with itself
+// leaves {x[l], x[l ^ 16]} (then {., x[l ^ 32]}) in the two results at every
+// lane, with no LDS round trip (ds_bpermute) in the softmax's dependency
+// chain.  The four lanes end with bitwise-equal values (the pairs are the
+// same, max and + commute).
+__device__ __forceinline__ float lane_group_max(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float lane_group_sum(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Wait until at most N of this wave's vector-memory operations are outstanding
@@ -191,14 +231,16 @@ template <> struct mfma_t<f16> {
 // LK: 0 plain launch, with no lookup code (it cost 3% on the C5 batch); 1
 // cache_batch_idx / cu_seqlens_q lookups; 2 those and a page table (kernels of
 // their own, so the lookup kernels keep their code).
+// Register budget: waves per SIMD the 128-row kernels are built for (two
+// 8-wave workgroups per CU, their LDS rings fitting), and the 64-row ones
+// (launches of few workgroups, one per CU: registers are not what limits them).
 #ifndef NC_CHUNK_WAVES_PER_EU
-#define NC_CHUNK_WAVES_PER_EU 4  // > 0: register budget for this many waves per SIMD
+#define NC_CHUNK_WAVES_PER_EU 4
 #endif
-#if NC_CHUNK_WAVES_PER_EU > 0
-#define NC_CHUNK_OCC __attribute__((amdgpu_waves_per_eu(NC_CHUNK_WAVES_PER_EU)))
-#else
-#define NC_CHUNK_OCC
+#ifndef NC_CHUNK_WAVES_PER_EU_SMALL
+#define NC_CHUNK_WAVES_PER_EU_SMALL 2
 #endif
+#define NC_CHUNK_OCC __attribute__((amdgpu_waves_per_eu(ROWS == 64 ? NC_CHUNK_WAVES_PER_EU_SMALL : NC_CHUNK_WAVES_PER_EU)))
 
 template <typename TC, int D, int GB, int LK, int ROWS>
 __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_kernel(const ChunkParams p) {
@@ -239,6 +281,11 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
   const int rw = wave % kRowWaves;        // row block of this wave
   const int kg = wave / kRowWaves;        // key group of this wave
   const int kgo = kg * KG;                // its first key within a tile
+
+  // the arguments of the prologue, in one batch of scalar loads
+  pin_args(p.fd_members, p.fd_qtiles, p.fd_hblocks, p.fd_kv_heads, p.n_groups, p.seqlens, p.t_new, p.t_max,
+           p.window, p.keys_per_split, p.q, p.q_sb, p.q_st, p.q_sh, p.kc, p.vc, p.kc_sb, p.kc_st, p.kc_sh, p.vc_sb,
+           p.vc_st, p.vc_sh, p.n_heads, p.group, p.fused);
 
   // ---- block -> (group = (b, kv head, head block), key split, q tile) ----
   // A group's blocks run on one XCD (workgroups go round-robin over the 8 XCDs)
@@ -457,14 +504,38 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
 
   auto compute = [&](int kt0, const char* ks, const char* vs) __attribute__((always_inline)) {
     // ---- S^T = K . Q^T for the KB key blocks of the tile ----
+    // 64-row kernels (register budget of 2 waves per SIMD): software-pipelined
+    // operand reads, block kb + 1's K reads issued before block kb's MFMAs (the
+    // scheduling barriers keep that order; left alone, the compiler waited for
+    // each read right before its MFMA, one LDS round trip per MFMA).  The
+    // 128-row kernels have no registers for it (spills) and keep the
+    // compiler's order.
+    constexpr bool kPipe = ROWS == 64;
     f4v acc_s[KB];
+    uint4 ka[2][DC];
+    auto k_load = [&](int kb, uint4 (&dst)[DC]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) {
-      acc_s[kb] = f4v{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < DC; ++c) dst[c] = *reinterpret_cast<const uint4*>(ks + (kgo + 16 * kb) * ROWB + k_rd(c));
+    };
+    if constexpr (kPipe) {
+      k_load(0, ka[0]);
 #pragma unroll
-      for (int c = 0; c < DC; ++c) {
-        const uint4 a = *reinterpret_cast<const uint4*>(ks + (kgo + 16 * kb) * ROWB + k_rd(c));
-        mfma_t<TC>::run(__builtin_bit_cast(v8, a), qf[c], acc_s[kb]);
+      for (int kb = 0; kb < KB; ++kb) {
+        if (kb + 1 < KB) k_load(kb + 1, ka[(kb + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        acc_s[kb] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < DC; ++c) mfma_t<TC>::run(__builtin_bit_cast(v8, ka[kb & 1][c]), qf[c], acc_s[kb]);
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        acc_s[kb] = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          const uint4 a = *reinterpret_cast<const uint4*>(ks + (kgo + 16 * kb) * ROWB + k_rd(c));
+          mfma_t<TC>::run(__builtin_bit_cast(v8, a), qf[c], acc_s[kb]);
+        }
       }
     }
 
@@ -489,8 +560,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
         mt = fmaxf(mt, sv[kb][r]);
       }
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    mt = lane_group_max(mt);
     const float m_new = fmaxf(m_run, mt * p.scale_log2);
     const float alpha = fast_exp2(m_run - m_new);
     float rs = 0.0f;
@@ -506,8 +576,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
       pk[kb][0] = mfma_t<TC>::pack2(pv[0], pv[1]);
       pk[kb][1] = mfma_t<TC>::pack2(pv[2], pv[3]);
     }
-    rs += __shfl_xor(rs, 16, kWave);
-    rs += __shfl_xor(rs, 32, kWave);
+    rs = lane_group_sum(rs);
     l_run = l_run * alpha + rs;
     // rescale the output only when some row's running max moved
     if (__any(m_new != m_run)) {
@@ -519,17 +588,45 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
     m_run = m_new;
 
     // ---- O^T += V^T . P^T over the KC 32-key chunks ----
+    // V^T operands in groups of VG output blocks, the next group's reads
+    // issued before this group's MFMAs (as for K above).  Lane lr of group lq
+    // points at key (kgo + 32kc + 4lq + lr/4), dims 16db + 4*(lr%4) .. +3.
+    constexpr int VG = DB < 4 ? DB : 4;   // output blocks per group
+    constexpr int NG = KC * DB / VG;      // groups per tile
+    v8 va[2][VG];
+    auto v_load = [&](int gi, v8 (&dst)[VG]) __attribute__((always_inline)) {
+      const int kc = gi / (DB / VG), db0 = (gi % (DB / VG)) * VG;
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc) {
-      const v8 bp = __builtin_bit_cast(v8, make_uint4(pk[2 * kc][0], pk[2 * kc][1], pk[2 * kc + 1][0], pk[2 * kc + 1][1]));
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        // lane lr of group lq points at key (kgo + 32kc + 4lq + lr/4), dims 16db + 4*(lr%4) .. +3
-        const char* src0 = vs + (kgo + 32 * kc) * ROWB + v_rd(db);
+      for (int i = 0; i < VG; ++i) {
+        const char* src0 = vs + (kgo + 32 * kc) * ROWB + v_rd(db0 + i);
         const i16x4 lo4 = lds_read_tr16(src0);
         const i16x4 hi4 = lds_read_tr16(src0 + 16 * ROWB);
-        const v8 av = __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-        mfma_t<TC>::run(av, bp, acc_o[db]);
+        dst[i] = __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+    };
+    if constexpr (kPipe) {
+      v_load(0, va[0]);
+#pragma unroll
+      for (int gi = 0; gi < NG; ++gi) {
+        if (gi + 1 < NG) v_load(gi + 1, va[(gi + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+        const int kc = gi / (DB / VG), db0 = (gi % (DB / VG)) * VG;
+        const v8 bp = __builtin_bit_cast(v8, make_uint4(pk[2 * kc][0], pk[2 * kc][1], pk[2 * kc + 1][0], pk[2 * kc + 1][1]));
+#pragma unroll
+        for (int i = 0; i < VG; ++i) mfma_t<TC>::run(va[gi & 1][i], bp, acc_o[db0 + i]);
+      }
+    } else {
+#pragma unroll
+      for (int kc = 0; kc < KC; ++kc) {
+        const v8 bp = __builtin_bit_cast(v8, make_uint4(pk[2 * kc][0], pk[2 * kc][1], pk[2 * kc + 1][0], pk[2 * kc + 1][1]));
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const char* src0 = vs + (kgo + 32 * kc) * ROWB + v_rd(db);
+          const i16x4 lo4 = lds_read_tr16(src0);
+          const i16x4 hi4 = lds_read_tr16(src0 + 16 * ROWB);
+          const v8 av = __builtin_bit_cast(v8, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+          mfma_t<TC>::run(av, bp, acc_o[db]);
+        }
       }
     }
   };

@@ -82,7 +82,10 @@ hipError_t launch_chunk(const nc_attn_args& a, const AttnPlan& plan, const AttnS
 // rows, 4.01 at 128.
 constexpr int kChunkRowsSmall = 64;
 constexpr int kChunkRowsLarge = 128;
-constexpr int64_t kChunkLargeAt = 512;
+#ifndef NC_CHUNK_LARGE_AT
+#define NC_CHUNK_LARGE_AT 512
+#endif
+constexpr int64_t kChunkLargeAt = NC_CHUNK_LARGE_AT;
 // Split merge of the chunk kernel's partials (plan.chunk_splits > 1).
 hipError_t launch_chunk_merge(const nc_attn_args& a, const AttnPlan& plan, const AttnScratch& s,
                               hipStream_t stream, const RowFilter* rows = nullptr);
