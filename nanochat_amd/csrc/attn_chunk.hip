@@ -74,12 +74,16 @@ constexpr int kChunkWaves = 8;
 #define NC_CHUNK_TILE_KEYS 64
 #endif
 #ifndef NC_CHUNK_STAGES
-#define NC_CHUNK_STAGES 2
+#define NC_CHUNK_STAGES 2         // 128-row kernels (two workgroups per CU share the LDS)
+#endif
+#ifndef NC_CHUNK_STAGES_SMALL
+#define NC_CHUNK_STAGES_SMALL 3   // 64-row kernels (one workgroup per CU: 96 KiB of ring)
 #endif
 constexpr int kBN = NC_CHUNK_TILE_KEYS;   // keys per tile (a multiple of 32)
-constexpr int kStages = NC_CHUNK_STAGES;  // K/V tiles of the LDS ring (>= 2): kStages - 1 in flight
 constexpr int kChunkStagePages = 512;  // page numbers a workgroup stages in LDS (paged cache)
 constexpr float kNegBigC = -1.0e30f;
+// exponent-base slack of the online softmax (log2 units: P <= 256)
+constexpr float kRebaseSlack = 8.0f;
 constexpr int kXcdsC = 8;
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -237,6 +241,9 @@ template <> struct mfma_t<f16> {
 #ifndef NC_CHUNK_WAVES_PER_EU
 #define NC_CHUNK_WAVES_PER_EU 4
 #endif
+#ifndef NC_CHUNK_PIPE_LARGE
+#define NC_CHUNK_PIPE_LARGE 0  // 1: 128-row kernels pipeline their operand reads too (needs the 2-wave budget)
+#endif
 #ifndef NC_CHUNK_WAVES_PER_EU_SMALL
 #define NC_CHUNK_WAVES_PER_EU_SMALL 2
 #endif
@@ -260,6 +267,8 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
   constexpr int NI = kBN * CPR / kWave / kChunkWaves;  // direct loads per wave per tile, K (V the same)
   constexpr int LPT = 2 * NI;             // vector-memory operations per wave per tile
   static_assert(NI * kWave * kChunkWaves == kBN * CPR && KG % 32 == 0, "tile / workgroup shape");
+  // K/V tiles of the LDS ring (>= 2): kStages - 1 in flight
+  constexpr int kStages = ROWS == 64 ? NC_CHUNK_STAGES_SMALL : NC_CHUNK_STAGES;
   static_assert(kStages >= 2 && (kStages - 2) * LPT < 64, "ring depth");
 
   // ring of kStages tiles, one __shared__ array per stage (K at [0], V at [1]):
@@ -468,6 +477,18 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
       }
       return;
     }
+    if (ROWS == 64 && kt0 >= new_lo && kt0 + kBN <= hi) {
+      // whole tile inside the span and of new tokens (a prefill's tiles): k/v rows kt0 - s on
+      // (64-row kernels: the 128-row ones have no registers for a second fast path)
+      const char* kt = knew + static_cast<int64_t>(kt0 - s) * knst;
+      const char* vt = vnew + static_cast<int64_t>(kt0 - s) * vnst;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        dma16(kt + (lrow(i) * knst + lcol(i)), kd + i * kWave * 16);
+        dma16(vt + (lrow(i) * vnst + lcol(i)), vd + i * kWave * 16);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
       const int j = min(kt0 + lrow(i), hi - 1);
@@ -510,7 +531,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
     // each read right before its MFMA, one LDS round trip per MFMA).  The
     // 128-row kernels have no registers for it (spills) and keep the
     // compiler's order.
-    constexpr bool kPipe = ROWS == 64;
+    constexpr bool kPipe = ROWS == 64 || NC_CHUNK_PIPE_LARGE;
     f4v acc_s[KB];
     uint4 ka[2][DC];
     auto k_load = [&](int kb, uint4 (&dst)[DC]) __attribute__((always_inline)) {
@@ -561,8 +582,22 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
       }
     }
     mt = lane_group_max(mt);
-    const float m_new = fmaxf(m_run, mt * p.scale_log2);
-    const float alpha = fast_exp2(m_run - m_new);
+    // Lazy rebase: the exponent base m_run (log2 units) moves to the row's
+    // running max only when that max exceeds it by more than kRebaseSlack, so
+    // the rescale of the output accumulators runs on few tiles (in practice
+    // the first ones) instead of on every tile where some row's max grows.
+    // Until then P <= 2^kRebaseSlack, well inside fp32 sums and the P dtype's
+    // range; (m, l, o) stay consistent for any base, which is all the merges
+    // rely on.
+    const float m_tile = mt * p.scale_log2;
+    if (__any(m_tile > m_run + kRebaseSlack)) {
+      const float m_new = fmaxf(m_run, m_tile);
+      const float alpha = fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc_o[db] *= alpha;
+      m_run = m_new;
+    }
     float rs = 0.0f;
     uint32_t pk[KB][2];  // P packed in the cache dtype: [key block][pair of r]
 #pragma unroll
@@ -570,22 +605,14 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
       float pv[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pv[r] = fast_exp2(__builtin_fmaf(sv[kb][r], p.scale_log2, -m_new));
+        pv[r] = fast_exp2(__builtin_fmaf(sv[kb][r], p.scale_log2, -m_run));
         rs += pv[r];
       }
       pk[kb][0] = mfma_t<TC>::pack2(pv[0], pv[1]);
       pk[kb][1] = mfma_t<TC>::pack2(pv[2], pv[3]);
     }
     rs = lane_group_sum(rs);
-    l_run = l_run * alpha + rs;
-    // rescale the output only when some row's running max moved
-    if (__any(m_new != m_run)) {
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        acc_o[db] *= alpha;
-      }
-    }
-    m_run = m_new;
+    l_run += rs;
 
     // ---- O^T += V^T . P^T over the KC 32-key chunks ----
     // V^T operands in groups of VG output blocks, the next group's reads
