@@ -71,15 +71,19 @@ namespace {
 // a 4-wave workgroup, to hide latency, without more LDS).
 constexpr int kChunkWaves = 8;
 #ifndef NC_CHUNK_TILE_KEYS
-#define NC_CHUNK_TILE_KEYS 64
+#define NC_CHUNK_TILE_KEYS 64         // keys per tile, 128-row kernels
+#endif
+#ifndef NC_CHUNK_TILE_KEYS_SMALL
+#define NC_CHUNK_TILE_KEYS_SMALL 64   // keys per tile, 64-row kernels
 #endif
 #ifndef NC_CHUNK_STAGES
 #define NC_CHUNK_STAGES 2         // 128-row kernels (two workgroups per CU share the LDS)
 #endif
-#ifndef NC_CHUNK_STAGES_SMALL
-#define NC_CHUNK_STAGES_SMALL 3   // 64-row kernels (one workgroup per CU: 96 KiB of ring)
+#ifndef NC_CHUNK_STAGES_SMALL  // 64-row kernels (one workgroup per CU: at most 160 KiB of ring)
+#define NC_CHUNK_STAGES_SMALL (NC_CHUNK_TILE_KEYS_SMALL >= 128 ? 2 : 3)
 #endif
-constexpr int kBN = NC_CHUNK_TILE_KEYS;   // keys per tile (a multiple of 32)
+// keys per tile (multiples of 32), the larger of the two
+constexpr int kBNMax = NC_CHUNK_TILE_KEYS > NC_CHUNK_TILE_KEYS_SMALL ? NC_CHUNK_TILE_KEYS : NC_CHUNK_TILE_KEYS_SMALL;
 constexpr int kChunkStagePages = 512;  // page numbers a workgroup stages in LDS (paged cache)
 constexpr float kNegBigC = -1.0e30f;
 // exponent-base slack of the online softmax (log2 units: P <= 256)
@@ -111,6 +115,9 @@ __device__ __forceinline__ i16x4 lds_read_tr16(const char* p) {
 __device__ __forceinline__ uint32_t lds_addr(const char* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_char*)(p)));
 }
+// `dst` is wave-uniform by contract; readfirstlane states it to the compiler,
+// whose uniformity analysis does not always see it (an "s" operand it could
+// not prove uniform was handed a VGPR).
 // m0 (the LDS base of the load) is a reserved register: nothing else in these
 // kernels reads it (LDS instructions do not use m0 on gfx9 and later), so
 // clobbering it here is safe and the compiler's warning about it is silenced.
@@ -119,7 +126,7 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 __device__ __forceinline__ void dma16(const char* src, char* dst) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                :
-               : "v"(src), "s"(lds_addr(dst))
+               : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(dst)))
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -258,6 +265,7 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
   constexpr int QB = ROWS / GB;           // queries per workgroup
   constexpr int DC = D / 32;              // 32-dim chunks (MFMA K for S)
   constexpr int DB = D / 16;              // 16-dim output blocks
+  constexpr int kBN = ROWS == 64 ? NC_CHUNK_TILE_KEYS_SMALL : NC_CHUNK_TILE_KEYS;  // keys per tile
   constexpr int KG = kBN / kKeyGroups;    // keys of a tile one wave group scores
   constexpr int KB = KG / 16;             // 16-key blocks per wave and tile (S MFMAs)
   constexpr int KC = KG / 32;             // 32-key chunks per wave and tile (P.V MFMAs)
@@ -267,6 +275,8 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
   constexpr int NI = kBN * CPR / kWave / kChunkWaves;  // direct loads per wave per tile, K (V the same)
   constexpr int LPT = 2 * NI;             // vector-memory operations per wave per tile
   static_assert(NI * kWave * kChunkWaves == kBN * CPR && KG % 32 == 0, "tile / workgroup shape");
+  // software-pipelined operand reads (64-row kernels)
+  constexpr bool kPipe = ROWS == 64 || NC_CHUNK_PIPE_LARGE;
   // K/V tiles of the LDS ring (>= 2): kStages - 1 in flight
   constexpr int kStages = ROWS == 64 ? NC_CHUNK_STAGES_SMALL : NC_CHUNK_STAGES;
   static_assert(kStages >= 2 && (kStages - 2) * LPT < 64, "ring depth");
@@ -523,16 +533,14 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
     return v_row * ROWB + (((2 * db + (lr % 4) / 2) ^ v_sw) * 16) + ((lr % 4) % 2) * 8;
   };
 
-  auto compute = [&](int kt0, const char* ks, const char* vs) __attribute__((always_inline)) {
-    // ---- S^T = K . Q^T for the KB key blocks of the tile ----
-    // 64-row kernels (register budget of 2 waves per SIMD): software-pipelined
-    // operand reads, block kb + 1's K reads issued before block kb's MFMAs (the
-    // scheduling barriers keep that order; left alone, the compiler waited for
-    // each read right before its MFMA, one LDS round trip per MFMA).  The
-    // 128-row kernels have no registers for it (spills) and keep the
-    // compiler's order.
-    constexpr bool kPipe = ROWS == 64 || NC_CHUNK_PIPE_LARGE;
-    f4v acc_s[KB];
+  // ---- S^T = K . Q^T for the KB key blocks of a tile ----
+  // 64-row kernels (register budget of 2 waves per SIMD): software-pipelined
+  // operand reads, block kb + 1's K reads issued before block kb's MFMAs (the
+  // scheduling barriers keep that order; left alone, the compiler waited for
+  // each read right before its MFMA, one LDS round trip per MFMA).  The
+  // 128-row kernels have no registers for it (spills) and keep the
+  // compiler's order.
+  auto s_phase = [&](const char* ks, f4v (&acc_s)[KB]) __attribute__((always_inline)) {
     uint4 ka[2][DC];
     auto k_load = [&](int kb, uint4 (&dst)[DC]) __attribute__((always_inline)) {
 #pragma unroll
@@ -559,8 +567,10 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
         }
       }
     }
+  };
 
-    // ---- mask, scale, online softmax (each lane: one query row) ----
+  // ---- mask, scale, online softmax (each lane: one query row), then O += P.V ----
+  auto finish = [&](int kt0, const f4v (&acc_s)[KB], const char* vs) __attribute__((always_inline)) {
     const bool interior = wave_rows_full && kt0 + kBN <= hi && kt0 + kBN - 1 <= qpos_first &&
                           (p.window < 0 || kt0 >= qpos_last - p.window);
     // raw scores (the scale is positive: the running max is taken before scaling
@@ -657,26 +667,16 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
       }
     }
   };
+  auto compute = [&](int kt0, const char* ks, const char* vs) __attribute__((always_inline)) {
+    f4v acc_s[KB];
+    s_phase(ks, acc_s);
+    finish(kt0, acc_s, vs);
+  };
 
   bool stores_pending = false;  // cache stores of new tokens issued after the loads still counted on
-  // one tile: wait for its loads, free the oldest stage, refill it kStages - 1 tiles ahead, compute
-  auto step = [&](int t, auto st) __attribute__((always_inline)) {
-    constexpr int S = decltype(st)::value;
-    const int kt0 = lo + t * kBN;
-    // this wave's loads of tile t have landed: later tiles' loads (at most
-    // kStages - 2 of them, LPT operations each) may still be in flight
-    const int later = min(kStages - 2, ntiles - 1 - t);
-    if (stores_pending || later <= 0) {
-      wait_vmcnt<0>();
-      stores_pending = false;
-    } else if (later == 1) {
-      wait_vmcnt<LPT>();
-    } else {
-      wait_vmcnt<(kStages >= 4 ? 2 * LPT : LPT)>();
-    }
-    __syncthreads();  // every wave's loads of tile t landed; tile t - 1's stage is free
-    char* ks = stage_k(st);
-    char* vs = stage_v(st);
+  // a landed tile: keys past the span (or outside the page pool) zeroed, and
+  // this workgroup's new tokens stored into the cache
+  auto fix_tile = [&](int kt0, char* ks, char* vs) __attribute__((always_inline)) {
     char* kme = ks + wave * NI * kWave * 16 + lane * 16;  // this lane's landed chunks (slot i at + i * 1 KiB)
     char* vme = vs + wave * NI * kWave * 16 + lane * 16;
     if (kt0 + kBN > hi || (LK == 2 && pages_bad)) {
@@ -708,6 +708,26 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
       }
       stores_pending = true;
     }
+  };
+  // one tile: wait for its loads, free the oldest stage, refill it kStages - 1 tiles ahead, compute
+  auto step = [&](int t, auto st) __attribute__((always_inline)) {
+    constexpr int S = decltype(st)::value;
+    const int kt0 = lo + t * kBN;
+    // this wave's loads of tile t have landed: later tiles' loads (at most
+    // kStages - 2 of them, LPT operations each) may still be in flight
+    const int later = min(kStages - 2, ntiles - 1 - t);
+    if (stores_pending || later <= 0) {
+      wait_vmcnt<0>();
+      stores_pending = false;
+    } else if (later == 1) {
+      wait_vmcnt<LPT>();
+    } else {
+      wait_vmcnt<(kStages >= 4 ? 2 * LPT : LPT)>();
+    }
+    __syncthreads();  // every wave's loads of tile t landed; tile t - 1's stage is free
+    char* ks = stage_k(st);
+    char* vs = stage_v(st);
+    fix_tile(kt0, ks, vs);
     if (t + kStages - 1 < ntiles) issue(t + kStages - 1, std::integral_constant<int, (S + kStages - 1) % kStages>{});
     compute(kt0, ks, vs);
   };
@@ -961,7 +981,7 @@ ChunkParams make_chunk_params(const nc_attn_args& a, const AttnPlan& plan, const
 
 bool chunk_supports(const nc_attn_args& a) {
   // a key tile's byte span (64 cache rows) must fit the kernel's 32-bit offsets
-  const int64_t tile_bytes = kBN * std::max(std::abs(a.kc_stride_t), std::abs(a.vc_stride_t)) * 2;
+  const int64_t tile_bytes = kBNMax * std::max(std::abs(a.kc_stride_t), std::abs(a.vc_stride_t)) * 2;
   return a.t_new > 1 && a.q_dtype == a.cache_dtype &&
          (a.cache_dtype == NC_DTYPE_BF16 || a.cache_dtype == NC_DTYPE_F16) &&
          (a.head_dim == 64 || a.head_dim == 128) && tile_bytes < (int64_t(1) << 31);
