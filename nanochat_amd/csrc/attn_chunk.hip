@@ -787,19 +787,27 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
   }
 }
 
-// Split merge of the chunk kernel's partials: block (group, q tile, 64-row
-// slice) combines the slots of the slice's 64 (query, head) rows with the
-// log-sum-exp rule.  A chunk workgroup's key span, hence its split count, is
-// the same for all its rows, so a block whose tile ran unsplit returns after
-// one read of cache_seqlens.  Four threads per row, each folding D / 4
-// consecutive dims over the splits, kMergeCH splits per memory round trip.
-constexpr int kMergeCH = 4;
+// Split merge of the chunk kernel's partials: block (group, q tile, slice of
+// kMergeRows rows) combines the slots of the slice's (query, head) rows with
+// the log-sum-exp rule.  A chunk workgroup's key span, hence its split count,
+// is the same for all its rows, so a block whose tile ran unsplit returns after
+// one read of cache_seqlens.  kMergeTPR threads per row, each folding D /
+// kMergeTPR consecutive dims over the splits; every slot load of a chunk of
+// kMergeCH splits is in flight together (the slot index clamped to the last
+// split, not branched on), so up to kMergeCH splits cost one memory round trip
+// after the cache_seqlens read.
+constexpr int kMergeRows = 32;
+constexpr int kMergeTPR = 16;
+constexpr int kMergeCH = 16;
 
 template <typename TC, int D, int GB, int ROWS, bool IND>
-__global__ __launch_bounds__(256) void chunk_merge_kernel(const ChunkParams p) {
+__global__ __launch_bounds__(kMergeRows * kMergeTPR) void chunk_merge_kernel(const ChunkParams p) {
   constexpr int QB = ROWS / GB;
-  constexpr int SLICES = ROWS / 64;
-  constexpr int DT = D / 4;               // dims per thread
+  constexpr int SLICES = ROWS / kMergeRows;
+  constexpr int DT = D / kMergeTPR;       // dims per thread
+  static_assert(DT % 4 == 0 && ROWS % kMergeRows == 0, "merge shape");
+  pin_args(p.fd_qtiles, p.n_groups, p.n_hblocks, p.n_kv_heads, p.t_new, p.seqlens, p.t_max, p.window,
+           p.keys_per_split, p.group, p.n_heads, p.num_splits, p.part_ml, p.part_o, p.out);
   const uint32_t pb = blockIdx.x;
   const int slice = static_cast<int>(pb % SLICES);
   uint32_t rem;
@@ -823,11 +831,11 @@ __global__ __launch_bounds__(256) void chunk_merge_kernel(const ChunkParams p) {
   const int q_end = min(q0 + QB, rq.len);
   const int nsplit = chunk_span(p.seqlens[b], q0, q_end, p.t_max, p.window, p.keys_per_split).nsplit;
   if (nsplit <= 1) return;  // the chunk workgroup wrote these outputs itself
-  const int row = slice * 64 + static_cast<int>(threadIdx.x) / 4;
+  const int row = slice * kMergeRows + static_cast<int>(threadIdx.x) / kMergeTPR;
   const int qi = q0 + row / GB;
   if (qi >= rq.len) return;
   const int h = hk * p.group + hb * GB + row % GB;
-  const int d0 = (threadIdx.x % 4) * DT;
+  const int d0 = (static_cast<int>(threadIdx.x) % kMergeTPR) * DT;
   const int64_t pair_row = (b * p.t_new + qi) * p.n_heads + h;
   const float* ml = p.part_ml + pair_row * p.num_splits * 2;
   const float* po = p.part_o + pair_row * p.num_splits * D + d0;
@@ -839,16 +847,17 @@ __global__ __launch_bounds__(256) void chunk_merge_kernel(const ChunkParams p) {
     float4 os[kMergeCH][DT / 4];
 #pragma unroll
     for (int u = 0; u < kMergeCH; ++u) {
-      const int sp = sp0 + u;
-      const bool in = sp < nsplit;
-      const float2 v = in ? *reinterpret_cast<const float2*>(ml + 2 * sp) : make_float2(kNegBigC, 0.0f);
+      const int sp = min(sp0 + u, nsplit - 1);  // clamped: an in-bounds duplicate, masked below
+      const float2 v = *reinterpret_cast<const float2*>(ml + 2 * sp);
       ms[u] = v.x;
       ls[u] = v.y;
 #pragma unroll
-      for (int e = 0; e < DT / 4; ++e) {
-        os[u][e] = in ? *reinterpret_cast<const float4*>(po + static_cast<int64_t>(sp) * D + 4 * e)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      for (int e = 0; e < DT / 4; ++e) os[u][e] = *reinterpret_cast<const float4*>(po + static_cast<int64_t>(sp) * D + 4 * e);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // no use of a slot scheduled between the loads
+#pragma unroll
+    for (int u = 0; u < kMergeCH; ++u) {
+      if (sp0 + u >= nsplit) ls[u] = 0.0f;
     }
     float mx = M;
 #pragma unroll
@@ -859,7 +868,7 @@ __global__ __launch_bounds__(256) void chunk_merge_kernel(const ChunkParams p) {
     for (int e = 0; e < DT; ++e) O[e] *= a;
 #pragma unroll
     for (int u = 0; u < kMergeCH; ++u) {
-      const bool live = ls[u] > 0.0f;  // l == 0: every key of the split masked for this row
+      const bool live = ls[u] > 0.0f;  // l == 0: every key of the split masked for this row, or a duplicate
       const float w = live ? fast_exp2(ms[u] - mx) : 0.0f;
       L = __builtin_fmaf(ls[u], w, L);
 #pragma unroll
@@ -908,7 +917,7 @@ hipError_t launch_c(const ChunkParams& p, int gb, int rows, hipStream_t stream) 
 
 template <typename TC, int D, bool IND, int ROWS>
 hipError_t launch_merge_cr(const ChunkParams& p, int gb, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(p.n_groups * p.n_qtiles * (ROWS / 64))), block(256);
+  const dim3 grid(static_cast<unsigned>(p.n_groups * p.n_qtiles * (ROWS / kMergeRows))), block(kMergeRows * kMergeTPR);
   switch (gb) {
     case 8: hipLaunchKernelGGL((chunk_merge_kernel<TC, D, 8, ROWS, IND>), grid, block, 0, stream, p); break;
     case 4: hipLaunchKernelGGL((chunk_merge_kernel<TC, D, 4, ROWS, IND>), grid, block, 0, stream, p); break;
