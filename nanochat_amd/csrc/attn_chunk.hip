@@ -795,10 +795,15 @@ __global__ __launch_bounds__(kChunkWaves * kWave) NC_CHUNK_OCC void chunk_attn_k
 // kMergeTPR consecutive dims over the splits; every slot load of a chunk of
 // kMergeCH splits is in flight together (the slot index clamped to the last
 // split, not branched on), so up to kMergeCH splits cost one memory round trip
-// after the cache_seqlens read.
+// after the cache_seqlens read (C5's chunk rows have 8).
 constexpr int kMergeRows = 32;
 constexpr int kMergeTPR = 16;
-constexpr int kMergeCH = 16;
+// slots per round trip: 8 keeps the kernel at ~108 VGPRs, two 512-thread blocks per CU (16: 200
+// VGPRs, one block per CU; C5's merges 8.9 and 16.0 us against 7.4 and 11.7 at 8)
+#ifndef NC_CHUNK_MERGE_CH
+#define NC_CHUNK_MERGE_CH 8
+#endif
+constexpr int kMergeCH = NC_CHUNK_MERGE_CH;
 
 template <typename TC, int D, int GB, int ROWS, bool IND>
 __global__ __launch_bounds__(kMergeRows * kMergeTPR) void chunk_merge_kernel(const ChunkParams p) {
