@@ -70,6 +70,9 @@ DecodeParams make_params(const nc_attn_args& a, const AttnPlan& plan, const Attn
   p.num_splits = plan.num_splits;
   p.keys_per_split = plan.keys_per_split;
   p.fused = fused_append ? 1 : 0;
+  p.bal_rows = plan.bal ? static_cast<int32_t>(a.batch) : 0;
+  p.bal_min_tiles = NC_DECODE_BAL_MIN_TILES;
+  p.bal_den = static_cast<int32_t>(plan.n_wg - plan.n_groups);
   p.rope_cos = p.rope_sin = nullptr;
   p.rope = 0;
   p.rope_len = 1;

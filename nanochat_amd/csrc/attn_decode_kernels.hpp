@@ -110,6 +110,9 @@ struct DecodeParams {
   int32_t q_dtype;
   int32_t num_splits, keys_per_split;
   int32_t fused;
+  // length-balanced pieces (LK == 3 kernels): the call's rows, the least
+  // 64-key tiles per piece, and the grid size minus n_groups
+  int32_t bal_rows, bal_min_tiles, bal_den;
   // fused QK prologue (rotary, RMS norm, scale) on q and the appended k; rope == 0: off
   const void* rope_cos;
   const void* rope_sin;
@@ -210,6 +213,138 @@ __device__ __forceinline__ KeyRange key_range(const DecodeParams& p, int64_t b, 
   if (r.n > r.kps * p.num_splits) r.kps = ((r.n + p.num_splits - 1) / p.num_splits + 63) / 64 * 64;
   r.nsplit = r.n > 0 ? static_cast<int>(fdiv(static_cast<uint32_t>(r.n + r.kps - 1), p.fd_kps)) : 1;
   if (r.kps != p.keys_per_split) r.nsplit = (r.n + r.kps - 1) / r.kps;
+  return r;
+}
+
+// ---- length-balanced pieces (LK == 3: single-token plain decode) ----
+// Row b's key span of T_b 64-key tiles is cut into P_b = max(1, ceil(T_b / c))
+// pieces per unit, c being one value for the whole call: the least c >=
+// bal_min_tiles with U * sum_b T_b <= c * bal_den (U units per row).  Then
+// sum_b U * P_b <= U * sum_b T_b / c + B * U <= bal_den + n_groups = grid
+// size, so every piece has a workgroup.  Pieces are numbered row by row, unit
+// by unit, piece by piece; workgroup w takes piece w and writes its partial
+// to slot w, so the slots of one (row, unit) are contiguous.  Workgroups past
+// the last piece exit (they are the last ones dispatched).  Every workgroup
+// and merge block derives the numbering from cache_seqlens itself: one load
+// per lane for every 64 rows, a wave sum and a wave prefix sum, no LDS.
+constexpr int kBalPasses = kDecodeBalMaxRows / kWave;
+
+__device__ __forceinline__ int wave_sum_int(int x) {
+#pragma unroll
+  for (int off = kWave / 2; off >= 1; off /= 2) x += __shfl_xor(x, off, kWave);
+  return x;
+}
+
+__device__ __forceinline__ int wave_incl_scan(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < kWave; off *= 2) {
+    const int y = __shfl_up(x, off, kWave);
+    x += lane >= off ? y : 0;
+  }
+  return x;
+}
+
+// Per lane, rows lane + 64 i: cache_seqlens, pieces per unit, and the
+// inclusive prefix of pieces (all units) over the rows up to that one.
+struct BalScan {
+  int s[kBalPasses];
+  int pieces[kBalPasses];
+  int incl[kBalPasses];
+  int c;  // tiles per piece
+};
+
+__device__ __forceinline__ BalScan bal_scan(const DecodeParams& p, int lane) {
+  BalScan r;
+  const int nrows = p.bal_rows;
+  // every pass's load in flight together (row index clamped, masked below)
+#pragma unroll
+  for (int i = 0; i < kBalPasses; ++i) r.s[i] = p.seqlens[min(lane + i * kWave, nrows - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  int tiles[kBalPasses];
+  int tsum = 0;
+#pragma unroll
+  for (int i = 0; i < kBalPasses; ++i) {
+    // the key span of the row's query, as key_range computes it
+    const int qpos = r.s[i];
+    const int hi = min(qpos + 1, p.t_max);
+    const int lo = p.window >= 0 ? max(0, qpos - p.window) : 0;
+    tiles[i] = lane + i * kWave < nrows ? (max(hi - lo, 0) + 63) >> 6 : 0;
+    tsum += tiles[i];
+  }
+  const int total = wave_sum_int(tsum) * p.n_units;  // the plan bounds it below 2^31
+  r.c = max(p.bal_min_tiles, (total + p.bal_den - 1) / p.bal_den);
+  int carry = 0;
+#pragma unroll
+  for (int i = 0; i < kBalPasses; ++i) {
+    r.pieces[i] = lane + i * kWave < nrows ? max(1, (tiles[i] + r.c - 1) / r.c) : 0;
+    r.incl[i] = carry;
+    if (i * kWave < nrows) {
+      r.incl[i] = wave_incl_scan(r.pieces[i] * p.n_units, lane) + carry;
+      carry = __builtin_amdgcn_readlane(r.incl[i], kWave - 1);
+    }
+  }
+  return r;
+}
+
+// The piece of workgroup w: its row, unit, index within the (row, unit), and
+// that row's pieces per unit and cache_seqlens.
+struct BalPiece {
+  bool found;
+  int b, u, j, pieces, s, c;
+};
+
+__device__ __forceinline__ BalPiece bal_piece(const DecodeParams& p, int w, int lane) {
+  const BalScan sc = bal_scan(p, lane);
+  BalPiece r{false, 0, 0, 0, 1, 0, sc.c};
+  int first = 0;
+#pragma unroll
+  for (int i = 0; i < kBalPasses; ++i) {
+    if (!r.found && i * kWave < p.bal_rows) {
+      // the first row whose inclusive prefix exceeds w (the prefix never decreases)
+      const uint64_t hit = __ballot(sc.incl[i] > w);
+      if (hit != 0) {
+        const int l = __builtin_ctzll(hit);
+        r.found = true;
+        r.b = i * kWave + l;
+        r.pieces = __builtin_amdgcn_readlane(sc.pieces[i], l);
+        r.s = __builtin_amdgcn_readlane(sc.s[i], l);
+        first = __builtin_amdgcn_readlane(sc.incl[i], l) - r.pieces * p.n_units;
+      }
+    }
+  }
+  if (r.found) {
+    const int rem = w - first;
+    r.u = rem / r.pieces;
+    r.j = rem - r.u * r.pieces;
+  }
+  return r;
+}
+
+// Group (b, unit u) of a balanced call: its first slot and piece count.
+__device__ __forceinline__ void bal_group_slots(const DecodeParams& p, int b, int u, int lane, int& first,
+                                                int& pieces) {
+  const BalScan sc = bal_scan(p, lane);
+  first = 0;
+  pieces = 1;
+#pragma unroll
+  for (int i = 0; i < kBalPasses; ++i) {
+    if (b / kWave == i) {
+      const int l = b % kWave;
+      pieces = __builtin_amdgcn_readlane(sc.pieces[i], l);
+      first = __builtin_amdgcn_readlane(sc.incl[i], l) - (p.n_units - u) * pieces;
+    }
+  }
+}
+
+// Key range of a balanced piece: [lo + j * c * 64, ...) of its row's span.
+__device__ __forceinline__ KeyRange bal_range(const DecodeParams& p, const BalPiece& bp) {
+  KeyRange r;
+  r.qpos = bp.s;
+  r.hi = min(r.qpos + 1, p.t_max);
+  r.lo = p.window >= 0 ? max(0, r.qpos - p.window) : 0;
+  r.n = r.hi - r.lo;
+  r.kps = bp.c * 64;
+  r.nsplit = bp.pieces;
   return r;
 }
 
@@ -359,6 +494,112 @@ void launch_merge_i(const DecodeParams& p, hipStream_t stream) {
   }
 }
 
+// Merge of length-balanced pieces (LK == 3 decode kernels): block g combines
+// the contiguous partial slots of group g, which it locates from
+// cache_seqlens as the producers did.  S slices of TPG threads: thread (k, e)
+// owns VE outputs e of the group and folds the slots k, k + S, k + 2S, ...,
+// CH of them per round trip (every load of a round trip in flight together);
+// the slices then combine through LDS.  With GB * D = 512 (GQA 16/4 at 128),
+// 4 slices of 128 threads take up to 64 slots in one round trip.
+template <int D, int GB>
+struct BalMerge {
+  static constexpr int VE = 4;
+  static constexpr int TPG = GB * D / VE;
+  static constexpr int S = TPG >= 512 ? 1 : (512 / TPG > 16 ? 16 : 512 / TPG);
+  static constexpr int NT = S * TPG;
+  static constexpr int CH = 16;
+  static_assert(NT % kWave == 0 && NT <= 1024, "merge block");
+};
+
+template <int D, int GB>
+__global__ __launch_bounds__((BalMerge<D, GB>::NT)) void merge_bal_kernel(const DecodeParams p) {
+  using M_ = BalMerge<D, GB>;
+  constexpr int VE = M_::VE, TPG = M_::TPG, S = M_::S, CH = M_::CH;
+  constexpr int TPH = D / VE;  // threads per head
+  __shared__ float sm_m[S][TPG];
+  __shared__ float sm_l[S][TPG];
+  __shared__ float4 sm_o[S][TPG];
+  pin_args(p.fd_hblocks, p.fd_kv_heads, p.fd_t_new, p.seqlens, p.part_ml, p.part_o, p.out, p.bal_rows,
+           p.bal_min_tiles, p.bal_den, p.n_units, p.t_max, p.window, p.n_heads, p.group, p.q_dtype);
+  const GroupIdx gi = group_index(p, blockIdx.x);
+  int first, nsplit;
+  bal_group_slots(p, static_cast<int>(gi.b), gi.hk * p.n_hblocks + gi.hb, threadIdx.x % kWave, first, nsplit);
+  if (nsplit <= 1) return;  // one piece: its workgroup wrote the output
+  const int k = threadIdx.x / TPG, e = threadIdx.x % TPG;
+  const int g = e / TPH, d0 = (e % TPH) * VE;
+  const int64_t slot0 = static_cast<int64_t>(first) * GB + g;  // slot `first`, head g; slots step GB
+  const float* ml = p.part_ml + slot0 * 2;
+  const float* po = p.part_o + slot0 * D + d0;
+  float M = kNegBig, L = 0.0f, O[VE];
+#pragma unroll
+  for (int v = 0; v < VE; ++v) O[v] = 0.0f;
+  for (int sp0 = k; sp0 < nsplit; sp0 += S * CH) {
+    float ms[CH], ls[CH];
+    float4 os[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int sp = min(sp0 + u * S, nsplit - 1);  // clamped: an in-bounds duplicate, masked below
+      const float2 v = *reinterpret_cast<const float2*>(ml + static_cast<int64_t>(2 * GB) * sp);
+      ms[u] = v.x;
+      ls[u] = v.y;
+      os[u] = *reinterpret_cast<const float4*>(po + static_cast<int64_t>(GB) * D * sp);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      if (sp0 + u * S >= nsplit) ls[u] = 0.0f;
+    }
+    float mx = M;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) mx = ls[u] > 0.0f ? fmaxf(mx, ms[u]) : mx;
+    const float a = fast_exp2(M - mx);
+    L *= a;
+#pragma unroll
+    for (int v = 0; v < VE; ++v) O[v] *= a;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const bool live = ls[u] > 0.0f;
+      const float w = live ? fast_exp2(ms[u] - mx) : 0.0f;
+      L = __builtin_fmaf(ls[u], w, L);
+      const float ov[VE] = {os[u].x, os[u].y, os[u].z, os[u].w};
+#pragma unroll
+      for (int v = 0; v < VE; ++v) O[v] = live ? __builtin_fmaf(ov[v], w, O[v]) : O[v];
+    }
+    M = mx;
+  }
+  sm_m[k][e] = M;
+  sm_l[k][e] = L;
+  sm_o[k][e] = make_float4(O[0], O[1], O[2], O[3]);
+  __syncthreads();
+  if (k != 0) return;
+  float mx = kNegBig;
+#pragma unroll
+  for (int kk = 0; kk < S; ++kk) mx = sm_l[kk][e] > 0.0f ? fmaxf(mx, sm_m[kk][e]) : mx;
+  float Lt = 0.0f, Ot[VE] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int kk = 0; kk < S; ++kk) {
+    const float l = sm_l[kk][e];
+    const float w = l > 0.0f ? fast_exp2(sm_m[kk][e] - mx) : 0.0f;
+    const float4 o = sm_o[kk][e];
+    Lt = __builtin_fmaf(l, w, Lt);
+    Ot[0] = __builtin_fmaf(o.x, w, Ot[0]);
+    Ot[1] = __builtin_fmaf(o.y, w, Ot[1]);
+    Ot[2] = __builtin_fmaf(o.z, w, Ot[2]);
+    Ot[3] = __builtin_fmaf(o.w, w, Ot[3]);
+  }
+  const float inv = Lt > 0.0f ? 1.0f / Lt : 0.0f;
+  const int64_t opair0 = gi.b * p.n_heads + gi.hk * p.group + gi.hb * GB;  // t_new = 1, row b's query
+  const int64_t o0 = (opair0 + g) * D + d0;
+#pragma unroll
+  for (int v = 0; v < VE; ++v) store_any(p.out, o0 + v, p.q_dtype, Ot[v] * inv);
+}
+
+template <int D, int GB>
+void launch_merge_bal(const DecodeParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((merge_bal_kernel<D, GB>), dim3(static_cast<unsigned>(p.n_groups)), dim3(BalMerge<D, GB>::NT),
+                     0, stream, p);
+}
+
 template <int D, int GB>
 void launch_merge_g(const DecodeParams& p, hipStream_t stream) {
   if (p.indirect) {
@@ -387,10 +628,13 @@ constexpr int kInKernelMergeChunk = 8;
 constexpr int kMaxSplitPages = 64;
 
 // LK: 0 plain launch (no lookup code); 1 cache_batch_idx / cu_seqlens_q
-// lookups; 2 those and a page table.  Paged launches have kernels of their
-// own so the lookup kernels keep the code they had without paging.
+// lookups; 2 those and a page table; 3 plain launch of length-balanced
+// pieces.  Paged launches have kernels of their own so the lookup kernels
+// keep the code they had without paging.
 template <typename TC, bool QPK, int D, int GB, int NW, int LK>
-__global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodeParams p) {
+// (balanced pieces with 4-head blocks: the piece lookup's few registers would
+// take the kernel past 168 VGPRs, 2 waves per SIMD instead of 3)
+__global__ __launch_bounds__(NW * kWave, (LK == 3 && GB == 4) ? 3 : 1) void decode_attn_kernel(const DecodeParams p) {
   constexpr int VEC = widen<TC>::N;
   constexpr int LPK = D / VEC;            // lanes per key row
   constexpr int KPI = kWave / LPK;        // keys per load instruction
@@ -420,19 +664,32 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
            p.window, p.keys_per_split, p.num_splits, p.t_new, p.n_heads, p.group, p.fused, p.kc, p.vc, p.kc_sb,
            p.kc_sh, p.kc_st, p.vc_sb, p.vc_sh, p.vc_st);
 
+  constexpr bool kLookups = LK == 1 || LK == 2;
+  constexpr bool kBal = LK == 3;
+
   // ---- block -> (group, split) ----
+  uint32_t group;
+  int split;
+  [[maybe_unused]] BalPiece bp;
+  if constexpr (kBal) {
+    bp = bal_piece(p, static_cast<int>(blockIdx.x), lane);
+    if (!bp.found) return;  // past the call's last piece
+    group = static_cast<uint32_t>(bp.b * p.n_units + bp.u);
+    split = bp.j;
+  } else {
 #if NC_DECODE_XCD_MAP
-  const uint32_t pb = blockIdx.x;
-  uint32_t split_u;
-  const uint32_t gq = fdivmod(pb / kXcds, p.fd_splits, split_u);
-  const int split = static_cast<int>(split_u);
-  const uint32_t group = gq * kXcds + pb % kXcds;
-  if (group >= p.n_groups) return;
+    const uint32_t pb = blockIdx.x;
+    uint32_t split_u;
+    const uint32_t gq = fdivmod(pb / kXcds, p.fd_splits, split_u);
+    split = static_cast<int>(split_u);
+    group = gq * kXcds + pb % kXcds;
+    if (group >= p.n_groups) return;
 #else
-  uint32_t split_u;
-  const uint32_t group = fdivmod(blockIdx.x, p.fd_splits, split_u);
-  const int split = static_cast<int>(split_u);
+    uint32_t split_u;
+    group = fdivmod(blockIdx.x, p.fd_splits, split_u);
+    split = static_cast<int>(split_u);
 #endif
+  }
   const GroupIdx gi = group_index(p, group);
   const int64_t b = gi.b;
   const int t = gi.t, hk = gi.hk, hb = gi.hb;
@@ -440,7 +697,7 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   // invalid entry skips the row in every workgroup of it
   int64_t cb = b;
   RowQ rq{b * p.t_new, p.t_new};
-  if constexpr (LK != 0) {
+  if constexpr (kLookups) {
     const bool report = split == 0 && t == 0 && hk == 0 && hb == 0 && threadIdx.x == 0;
     if constexpr (LK == 2) {
       cb = 0;  // paged: every position is addressed through the page table
@@ -453,9 +710,21 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     if (rq.len < p.len_lo || rq.len > p.len_hi || t >= rq.len) return;
   }
 
-  const KeyRange kr = key_range(p, b, t);
-  const int64_t pair0 = (b * p.t_new + t) * p.n_heads + hk * p.group + hb * GB;  // (b, t, first q head): partials
+  const KeyRange kr = [&] {
+    if constexpr (kBal) {
+      return bal_range(p, bp);
+    } else {
+      return key_range(p, b, t);
+    }
+  }();
+  const int64_t pair0 = (b * p.t_new + t) * p.n_heads + hk * p.group + hb * GB;  // (b, t, first q head)
   const int64_t opair0 = (rq.tok0 + t) * p.n_heads + hk * p.group + hb * GB;     // its row of `out`
+  // partial slots: (pair, split) order, or (piece, head) order for balanced
+  // pieces (this piece is slot blockIdx.x, the group's pieces contiguous)
+  const int64_t slot_first = kBal ? (static_cast<int64_t>(blockIdx.x) - split) * GB : pair0 * p.num_splits;
+  const int64_t slot_head = kBal ? 1 : p.num_splits;  // head g's slots start at slot_first + g * slot_head
+  constexpr int64_t kSlotStep = kBal ? GB : 1;        // from one split's slot to the next one's
+  const int64_t slot_mine = slot_first + split * kSlotStep;
   if (split >= kr.nsplit) return;  // past this query's keys: the merge never reads this slot
   const int qpos = kr.qpos;
   const int k0 = kr.lo + split * kr.kps;
@@ -769,10 +1038,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
       float acc = 0.0f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) acc += sm_o[w][g][d] * sm_w[w][g];
-      p.part_o[((pair0 + g) * p.num_splits + split) * D + d] = acc;
+      p.part_o[(slot_mine + g * slot_head) * D + d] = acc;
     }
     if (tid < GB) {
-      *reinterpret_cast<float2*>(p.part_ml + ((pair0 + tid) * p.num_splits + split) * 2) =
+      *reinterpret_cast<float2*>(p.part_ml + (slot_mine + tid * slot_head) * 2) =
           make_float2(sm_m[0][tid], sm_L[tid]);
     }
     return;
@@ -784,10 +1053,10 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
     float acc = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) acc += sm_o[w][g][d] * sm_w[w][g];
-    coherent_store(p.part_o + ((pair0 + g) * p.num_splits + split) * D + d, acc);
+    coherent_store(p.part_o + (slot_mine + g * slot_head) * D + d, acc);
   }
   if (tid < GB) {
-    float* ml = p.part_ml + ((pair0 + tid) * p.num_splits + split) * 2;
+    float* ml = p.part_ml + (slot_mine + tid * slot_head) * 2;
     coherent_store(ml, sm_m[0][tid]);
     coherent_store(ml + 1, sm_L[tid]);
   }
@@ -808,8 +1077,8 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
   const int nsplit = kr.nsplit;
   for (int idx = tid; idx < GB * D; idx += NW * kWave) {
     const int g = idx / D, d = idx % D;
-    const float* ml = p.part_ml + (pair0 + g) * p.num_splits * 2;
-    const float* po = p.part_o + (pair0 + g) * p.num_splits * D + d;
+    const float* ml = p.part_ml + (slot_first + g * slot_head) * 2;
+    const float* po = p.part_o + (slot_first + g * slot_head) * D + d;
     float M = kNegBig, L = 0.0f, O = 0.0f;
     for (int sp0 = 0; sp0 < nsplit; sp0 += kInKernelMergeChunk) {
       float ms[kInKernelMergeChunk], ls[kInKernelMergeChunk], os[kInKernelMergeChunk];
@@ -817,9 +1086,9 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
       for (int u = 0; u < kInKernelMergeChunk; ++u) {
         // clamped, not branched: every load of the chunk in flight together
         const int sp = min(sp0 + u, nsplit - 1);
-        ms[u] = coherent_load(ml + 2 * sp);
-        ls[u] = coherent_load(ml + 2 * sp + 1);
-        os[u] = coherent_load(po + static_cast<int64_t>(sp) * D);
+        ms[u] = coherent_load(ml + 2 * kSlotStep * sp);
+        ls[u] = coherent_load(ml + 2 * kSlotStep * sp + 1);
+        os[u] = coherent_load(po + kSlotStep * D * sp);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -850,7 +1119,13 @@ __global__ __launch_bounds__(NW * kWave) void decode_attn_kernel(const DecodePar
 template <typename TC, bool QPK, int D, int GB, int LK>
 hipError_t launch_gi(const DecodeParams& p, int64_t n_wg, bool wide, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(n_wg));
-  if constexpr (GB <= 4 && GB * D <= kWideMaxElems) {
+  if constexpr (LK == 3) {  // balanced pieces: the plan never combines them with wide workgroups
+    hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWavesPerWG, LK>), grid, dim3(kWavesPerWG * kWave), 0,
+                       stream, p);
+    if (p.tickets == nullptr) launch_merge_bal<D, GB>(p, stream);
+    return hipGetLastError();
+  }
+  if constexpr (LK != 3 && GB <= 4 && GB * D <= kWideMaxElems) {
     if (wide) {
       hipLaunchKernelGGL((decode_attn_kernel<TC, QPK, D, GB, kWideWaves, LK>), grid, dim3(kWideWaves * kWave), 0,
                          stream, p);
@@ -866,6 +1141,7 @@ hipError_t launch_gi(const DecodeParams& p, int64_t n_wg, bool wide, hipStream_t
 
 template <typename TC, bool QPK, int D, int GB>
 hipError_t launch_g(const DecodeParams& p, int64_t n_wg, bool wide, hipStream_t stream) {
+  if (p.bal_rows > 0) return launch_gi<TC, QPK, D, GB, 3>(p, n_wg, wide, stream);
   if (p.pages.table != nullptr) return launch_gi<TC, QPK, D, GB, 2>(p, n_wg, wide, stream);
   return p.indirect ? launch_gi<TC, QPK, D, GB, 1>(p, n_wg, wide, stream)
                     : launch_gi<TC, QPK, D, GB, 0>(p, n_wg, wide, stream);

@@ -147,6 +147,17 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   plan->num_splits = static_cast<int>(ns);
   plan->n_wg = decode_grid(plan->n_groups, plan->num_splits);
   if (plan->n_groups <= 0 || plan->n_wg <= 0 || plan->n_wg > INT32_MAX) return NC_ERR_BAD_SHAPE;
+  // Length-balanced pieces where the uniform split count would stretch long
+  // rows' splits past keys_per_split (the grid cap binds) and there are rows
+  // to balance: n_groups * num_splits workgroups (no XCD rounding: pieces are
+  // not mapped to XCDs), one piece size for the call chosen on the device
+  // from cache_seqlens.  Rows of equal length get the pieces the splits had.
+  const int64_t row_tiles = (a.t_max + 63) / 64;
+  plan->bal = NC_DECODE_BAL && !plan->wide && a.t_new == 1 && a.keys_per_split == 0 &&
+              a.cache_batch_idx == nullptr && a.cu_seqlens_q == nullptr && a.page_table == nullptr &&
+              a.batch >= 2 && a.batch <= kDecodeBalMaxRows && ns >= 2 && max_keys > ns * kps &&
+              a.batch * row_tiles * plan->n_units <= INT32_MAX / 2;
+  if (plan->bal) plan->n_wg = plan->n_groups * ns;
 
   plan->use_chunk = a.t_new >= kChunkMinTokens && chunk_supports(a);
   plan->chunk_keys_per_split = 0;
@@ -184,12 +195,14 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
   }
   const int64_t merge_splits = plan->use_chunk ? plan->chunk_splits : ns;
   // decode splits: the last workgroup of each group merges (no merge launch)
-  plan->merge_in_kernel = !plan->use_chunk && ns > 1 && plan->n_groups <= kMaxTickets &&
+  plan->merge_in_kernel = !plan->use_chunk && !plan->bal && ns > 1 && plan->n_groups <= kMaxTickets &&
                           plan->n_groups * ns <= kMergeInKernelMaxWG;
   if (merge_splits > 1) {
     const size_t pairs = static_cast<size_t>(a.batch * a.t_new * a.n_heads);
-    plan->ml_bytes = round256(pairs * merge_splits * 2 * 4);
-    plan->o_bytes = round256(pairs * merge_splits * static_cast<size_t>(a.head_dim) * 4);
+    // balanced pieces: one slot per workgroup of the grid and head of its unit
+    const size_t slots = plan->bal ? static_cast<size_t>(plan->n_wg * hb) : pairs * merge_splits;
+    plan->ml_bytes = round256(slots * 2 * 4);
+    plan->o_bytes = round256(slots * static_cast<size_t>(a.head_dim) * 4);
   } else {
     plan->ml_bytes = plan->o_bytes = 0;
   }

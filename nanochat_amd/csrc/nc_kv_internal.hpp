@@ -37,6 +37,7 @@ struct AttnPlan {
   int num_splits;
   int64_t n_wg;        // decode grid size
   bool wide;           // decode with 8-wave workgroups and one split (few groups, short rows)
+  bool bal;            // decode with length-balanced pieces (see kDecodeBalMaxRows)
   bool merge_in_kernel;  // decode splits merged by their last workgroup (tickets), no merge launch
   bool use_chunk;      // T_new > 1 on the MFMA chunk kernel
   int chunk_rows;      // (query, head) rows per chunk workgroup: kChunkRowsSmall or kChunkRowsLarge
@@ -51,6 +52,20 @@ struct AttnPlan {
 
 // Returns NC_OK and fills `plan`, or an error code.
 int plan_attention(const nc_attn_args& a, AttnPlan* plan);
+
+// Single-token decode over rows of very unequal lengths: the uniform split
+// count of the plan leaves the long rows' workgroups with long splits that
+// finish last.  Such calls (plain layout, the library's split size, rows
+// longer than num_splits * keys_per_split possible, at most this many rows)
+// cut every row into pieces of one common size instead, sized on the device
+// from cache_seqlens so that all pieces fit the grid.
+constexpr int kDecodeBalMaxRows = 256;
+#ifndef NC_DECODE_BAL
+#define NC_DECODE_BAL 1  // 0: such calls keep the uniform split plan
+#endif
+#ifndef NC_DECODE_BAL_MIN_TILES
+#define NC_DECODE_BAL_MIN_TILES 4  // least 64-key tiles per piece
+#endif
 
 hipError_t launch_append(const nc_append_args& a, hipStream_t stream);
 hipError_t launch_fanout(const nc_fanout_args& a, int unit_bytes, hipStream_t stream);
