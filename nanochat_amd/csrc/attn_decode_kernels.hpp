@@ -46,6 +46,7 @@
 #pragma once
 
 #include <algorithm>
+#include <type_traits>
 
 #include "nc_kv_common.hpp"
 #include "nc_kv_internal.hpp"
@@ -131,6 +132,8 @@ constexpr int kWavesPerWG = NC_DECODE_WAVES;
 constexpr int kWideWaves = 8;
 constexpr int kWideMaxElems = 512;
 constexpr float kNegBig = -1.0e30f;   // finite "minus infinity" for running maxima
+// a decode tile moves its exponent base only past this many log2 units
+constexpr float kDecodeRebaseSlack = 8.0f;
 constexpr int kMaxMergeSplits = 256;  // split cap of the launch plan
 constexpr int kXcds = 8;              // MI355X: workgroups go round-robin over 8 XCDs
 
@@ -632,9 +635,10 @@ constexpr int kMaxSplitPages = 64;
 // pieces.  Paged launches have kernels of their own so the lookup kernels
 // keep the code they had without paging.
 template <typename TC, bool QPK, int D, int GB, int NW, int LK>
-// (balanced pieces with 4-head blocks: the piece lookup's few registers would
-// take the kernel past 168 VGPRs, 2 waves per SIMD instead of 3)
-__global__ __launch_bounds__(NW * kWave, (LK == 3 && GB == 4) ? 3 : 1) void decode_attn_kernel(const DecodeParams p) {
+// Occupancy floor per head block: 3 waves per SIMD (168 VGPRs) for blocks of
+// 4 q heads, 2 (256) for 8; the compiler otherwise spends registers on
+// issuing the next tile's loads early and drops a wave.
+__global__ __launch_bounds__(NW * kWave, GB == 4 ? 3 : (GB == 8 ? 2 : 1)) void decode_attn_kernel(const DecodeParams p) {
   constexpr int VEC = widen<TC>::N;
   constexpr int LPK = D / VEC;            // lanes per key row
   constexpr int KPI = kWave / LPK;        // keys per load instruction
@@ -807,40 +811,56 @@ __global__ __launch_bounds__(NW * kWave, (LK == 3 && GB == 4) ? 3 : 1) void deco
       }
       return;
     }
+    // the index is clamped to the split's last cached key (load_tile runs only
+    // while base < kc_end) rather than branched on: keys past the end load a
+    // duplicate that the tile step masks (weight 0), and the loads need no
+    // zero-filled copies
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const int j = base + i * KPI + row;
-      if (j < kc_end) {
-        kv[i] = load16(kbase + j * kst);
-        vv[i] = load16(vbase + j * vst);
-      } else {
-        kv[i] = make_uint4(0, 0, 0, 0);
-        vv[i] = make_uint4(0, 0, 0, 0);
-      }
+      const int j = min(base + i * KPI + row, kc_end - 1);
+      kv[i] = load16(kbase + j * kst);
+      vv[i] = load16(vbase + j * vst);
     }
   };
-  auto consume_tile = [&](int base, const uint4 (&kv)[NI], const uint4 (&vv)[NI]) {
+  // One tile step.  Scores stay unscaled (q . k) and the weights are
+  // exp2(s * scale_log2 - m) in one fma.  m[g] is an exponent base (log2
+  // units) that moves only when a score of the tile exceeds it by more than
+  // kDecodeRebaseSlack, so most tiles skip the rescale of o and l (the
+  // weights then reach up to 2^8 before the final normalisation).  Only a
+  // tile that runs past the split's end masks its keys (MASKED).
+  auto consume_tile = [&](auto masked, int base, const uint4 (&kv)[NI], const uint4 (&vv)[NI]) {
+    constexpr bool kMasked = decltype(masked)::value;
+    const float c2 = p.scale_log2;
     float sc[GB][NI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-      const bool valid = base + i * KPI + row < kc_end;
+      const bool valid = !kMasked || base + i * KPI + row < kc_end;
 #pragma unroll
       for (int g = 0; g < GB; ++g) {
-        const float d = group_sum<LPK>(qf[g].dot(kv[i])) * p.scale_log2;
+        const float d = group_sum<LPK>(qf[g].dot(kv[i]));
         sc[g][i] = valid ? d : -__builtin_inff();
       }
     }
+    float mt[GB];
+    bool grow = false;
 #pragma unroll
     for (int g = 0; g < GB; ++g) {
-      float mt = sc[g][0];
+      float x = sc[g][0];
 #pragma unroll
-      for (int i = 1; i < NI; ++i) mt = fmaxf(mt, sc[g][i]);
-      const float mn = fmaxf(m[g], mt);
-      const float alpha = fast_exp2(m[g] - mn);
-      m[g] = mn;
-      l[g] *= alpha;
+      for (int i = 1; i < NI; ++i) x = fmaxf(x, sc[g][i]);
+      mt[g] = x * c2;
+      grow = grow || mt[g] > m[g] + kDecodeRebaseSlack;
+    }
+    if (__any(grow)) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) o[g][e] *= alpha;
+      for (int g = 0; g < GB; ++g) {
+        const float mn = fmaxf(m[g], mt[g]);
+        const float alpha = fast_exp2(m[g] - mn);
+        m[g] = mn;
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[g][e] *= alpha;
+      }
     }
     if constexpr (QPK && NC_DECODE_PV_DOT2 && NI % 2 == 0) {
       // P.V on key pairs with v_dot2: P rounded to the cache dtype (as in
@@ -858,8 +878,8 @@ __global__ __launch_bounds__(NW * kWave, (LK == 3 && GB == 4) ? 3 : 1) void deco
         }
 #pragma unroll
         for (int g = 0; g < GB; ++g) {
-          const float p0 = fast_exp2(sc[g][i] - m[g]);
-          const float p1 = fast_exp2(sc[g][i + 1] - m[g]);
+          const float p0 = fast_exp2(__builtin_fmaf(sc[g][i], c2, -m[g]));
+          const float p1 = fast_exp2(__builtin_fmaf(sc[g][i + 1], c2, -m[g]));
           l[g] += p0 + p1;
           const uint32_t pp = dot_packed<TC>::pack(p0, p1);
 #pragma unroll
@@ -873,7 +893,7 @@ __global__ __launch_bounds__(NW * kWave, (LK == 3 && GB == 4) ? 3 : 1) void deco
         widen<TC>::run(vv[i], vf);
 #pragma unroll
         for (int g = 0; g < GB; ++g) {
-          const float pr = fast_exp2(sc[g][i] - m[g]);
+          const float pr = fast_exp2(__builtin_fmaf(sc[g][i], c2, -m[g]));
           l[g] += pr;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) o[g][e] = __builtin_fmaf(pr, vf[e], o[g][e]);
@@ -923,7 +943,7 @@ __global__ __launch_bounds__(NW * kWave, (LK == 3 && GB == 4) ? 3 : 1) void deco
   }
 
   while (base < kc_end) {
-    consume_tile(base, kv, vv);
+    consume_tile(std::true_type{}, base, kv, vv);
     base += STEP;
     if (base < kc_end) load_tile(base, kv, vv);
   }

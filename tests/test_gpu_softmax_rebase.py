@@ -1,8 +1,9 @@
-"""GPU parity of the chunk kernel's online softmax when the row maxima move.
+"""GPU parity of the online softmax of the chunk and decode kernels when the row maxima move.
 
-The chunk kernel keeps an exponent base per query row and moves it to the
-running max only when that max outgrows it by more than 2^8 (the output
-accumulators are rescaled then).  N(0,1) inputs barely exercise that: here the
+Both kernels keep an exponent base per query row (the decode kernel: per key
+group of a wave) and move it to the running max only when that max outgrows it
+by more than 2^8 (the output accumulators are rescaled then).  N(0,1) inputs
+barely exercise that: here the
 keys carry a component along the row's query direction whose weight depends on
 the key position, so the scores
 - ramp: grow by tens of log2 units per 64-key tile (a rebase on every tile),
@@ -10,8 +11,10 @@ the key position, so the scores
   with the earlier tiles' weight underflowing to zero),
 - drift: grow by a few log2 units over the whole row (no rebase after the
   first tile: P reaches up to 2^5 before normalisation),
-on the 64-row kernel (small calls), the 128-row kernel (>= 512 row units) and a
-split-K call (key span > 2048).
+on the chunk kernel's 64-row form (small calls), its 128-row form (>= 512 row
+units) and a split-K call (key span > 2048), and on single-token decode: the
+split plan with in-kernel merge (MHA), length-balanced pieces (GQA 16/4, skewed
+rows), 8-wave workgroups without split, and explicit 64-key splits.
 
 Reference: the oracle (nanochat/flash_attention.py:155-177 + :69-102 row by
 row) in float32 on the CPU, from the same inputs.  Tolerance as the other
@@ -66,6 +69,11 @@ SHAPES = {
     "rows64": (1, 256, 4, 4, 128, 1024, [0], 0),            # 64-row kernel, prefill into an empty cache
     "rows128": (16, 128, 16, 4, 128, 512, [300] * 16, 0),   # 16 x 128 / 16 x 4 = 512 units: 128-row kernel
     "split": (1, 64, 4, 1, 128, 4096, [3000], 1024),        # key span 3064 in 1024-key splits
+    "dec_mha": (4, 1, 8, 8, 128, 4096, [3000, 100, 2000, 4000], 0),     # 16 splits, merged in-kernel
+    "dec_gqa_bal": (24, 1, 16, 4, 128, 12288,                           # 96 groups, 42 splits: pieces
+                    [8000, 128, 300, 7000, 129, 1, 0, 5000] + [128 + 37 * i for i in range(16)], 0),
+    "dec_wide": (16, 1, 12, 12, 128, 2048, [1000 + 61 * i for i in range(16)], 0),  # 192 groups, no split
+    "dec_split64": (2, 1, 4, 4, 128, 4096, [4000, 300], 64),           # explicit 64-key splits (63 on row 0)
 }
 
 
