@@ -71,6 +71,12 @@
 #ifndef NC_DECODE_PV_DOT2
 #define NC_DECODE_PV_DOT2 1     // 1: P.V with v_dot2 on key pairs (packed caches)
 #endif
+#ifndef NC_DECODE_WIDE_EAGER
+// 1: 8-wave workgroups rescale on every tile instead of moving the exponent
+// base lazily (2 waves per SIMD: the per-tile vote and branch sit on the
+// critical path; C3 decode 0.3864 -> 0.3827 ms/step)
+#define NC_DECODE_WIDE_EAGER 1
+#endif
 #ifndef NC_DECODE_KEY_BYTES
 #define NC_DECODE_KEY_BYTES 65536  // default split: this many K bytes per unit (and as many V)
 #endif
@@ -851,7 +857,7 @@ __global__ __launch_bounds__(NW * kWave, GB == 4 ? 3 : (GB == 8 ? 2 : 1)) void d
       mt[g] = x * c2;
       grow = grow || mt[g] > m[g] + kDecodeRebaseSlack;
     }
-    if (__any(grow)) {
+    if (NC_DECODE_WIDE_EAGER && NW == kWideWaves ? true : __any(grow)) {
 #pragma unroll
       for (int g = 0; g < GB; ++g) {
         const float mn = fmaxf(m[g], mt[g]);
