@@ -62,6 +62,9 @@
 #ifndef NC_DECODE_NI_GQA
 #define NC_DECODE_NI_GQA 4      // same for head blocks of 4 or 8 q heads
 #endif
+#ifndef NC_DECODE_GQA4_WAVES
+#define NC_DECODE_GQA4_WAVES 3  // occupancy floor (waves per SIMD) of 4-head blocks
+#endif
 #ifndef NC_DECODE_XCD_MAP
 #define NC_DECODE_XCD_MAP 1     // 1: the splits of a unit run on the XCD of its merge block
 #endif
@@ -644,7 +647,7 @@ template <typename TC, bool QPK, int D, int GB, int NW, int LK>
 // Occupancy floor per head block: 3 waves per SIMD (168 VGPRs) for blocks of
 // 4 q heads, 2 (256) for 8; the compiler otherwise spends registers on
 // issuing the next tile's loads early and drops a wave.
-__global__ __launch_bounds__(NW * kWave, GB == 4 ? 3 : (GB == 8 ? 2 : 1)) void decode_attn_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(NW * kWave, GB == 4 ? NC_DECODE_GQA4_WAVES : (GB == 8 ? 2 : 1)) void decode_attn_kernel(const DecodeParams p) {
   constexpr int VEC = widen<TC>::N;
   constexpr int LPK = D / VEC;            // lanes per key row
   constexpr int KPI = kWave / LPK;        // keys per load instruction
