@@ -31,13 +31,6 @@ constexpr int64_t kChunkWGPerRow = 256;
 constexpr int64_t kChunkSplitAbove = 2048;
 // Default decode plans size their split count so the grid has about this
 // many workgroups (long rows then take longer splits).
-// Varlen chunk calls (cu_seqlens_q) keep half the workgroups per row for
-// 128-row workgroups: their grid spans every row of the batch, so more splits
-// also add workgroups that exit at once (C5 as one call per layer: 6.37 vs
-// 6.51 ms/step with the two-call target).
-#ifndef NC_CHUNK_VARLEN_HALF
-#define NC_CHUNK_VARLEN_HALF 1
-#endif
 #ifndef NC_DECODE_GRID_TARGET
 #define NC_DECODE_GRID_TARGET 4096
 #endif
@@ -187,12 +180,11 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
     if (ckps == 0) {
       // workgroups of one row per split: q tiles x kv heads x head blocks
       const int64_t per_row = (a.t_new + qb - 1) / qb * a.n_kv_heads * plan->n_hblocks;
-      // 128-row workgroups aim at as many per row as 64-row ones: C5's chunk rows get 1024-key
-      // splits (3.378 vs 3.467 ms/step at 2048 on one box, once the chunk merge had 8 slots
-      // per round trip; 2048 had measured ahead before that); varlen calls: see above
-      const int64_t wg_per_row = (NC_CHUNK_VARLEN_HALF && a.cu_seqlens_q != nullptr)
-                                     ? kChunkWGPerRow * kChunkRowsSmall / plan->chunk_rows
-                                     : kChunkWGPerRow;
+      // 128-row workgroups aim at half as many per row: C5's chunk rows get 2048-key splits
+      // (fewer partials for the merge).  Measured on one box, C5 chunk part, 1024 vs 2048:
+      // 3.378 vs 3.467 ms/step at 16 steps (lengths to 14336), but 3.064 vs 2.886 at 8 steps
+      // (lengths to 15360); one varlen call per layer 6.51 vs 6.37.
+      const int64_t wg_per_row = kChunkWGPerRow * kChunkRowsSmall / plan->chunk_rows;
       const int64_t want = (span * per_row + wg_per_row - 1) / wg_per_row;
       ckps = span > kChunkSplitAbove
                  ? std::min(span, std::max(kChunkSplitUnit, (want + kChunkSplitUnit - 1) / kChunkSplitUnit * kChunkSplitUnit))
