@@ -157,13 +157,10 @@ int plan_attention(const nc_attn_args& a, AttnPlan* plan) {
               a.cache_batch_idx == nullptr && a.cu_seqlens_q == nullptr && a.page_table == nullptr &&
               a.batch >= 2 && a.batch <= kDecodeBalMaxRows && ns >= 2 && max_keys > ns * kps &&
               a.batch * row_tiles * plan->n_units <= INT32_MAX / 2;
-  // Pieces beyond one per group: at most kDecodeBalPieces (fewer workgroups
-  // past the last piece, each of which still runs the lookup).  Measured on
-  // MI355X, C5 decode rows (192 groups; the grid 4032 -> 3328 workgroups, the
-  // same 256-key pieces): 1.778-1.793 -> 1.742-1.744 ms/step; 48 uniform
-  // 15000-key rows 254.8 -> 247.6 us per call.  A flat cap of 2304 also
-  // helped C5 but cost 8% on 1024 groups of ragged MHA rows.
-  if (plan->bal) plan->n_wg = std::min(plan->n_groups * ns, plan->n_groups + kDecodeBalPieces);
+  // (A cap of n_groups + 3136 workgroups, fewer of them past the last piece,
+  // measured 1.742 vs 1.785 ms/step on C5 at 16 steps but 1.88 vs 1.81 at
+  // bench.py's default 8 steps, with the same pieces: no cap.)
+  if (plan->bal) plan->n_wg = plan->n_groups * ns;
 
   plan->use_chunk = a.t_new >= kChunkMinTokens && chunk_supports(a);
   plan->chunk_keys_per_split = 0;

@@ -63,10 +63,6 @@ constexpr int kDecodeBalMaxRows = 256;
 #ifndef NC_DECODE_BAL
 #define NC_DECODE_BAL 1  // 0: such calls keep the uniform split plan
 #endif
-#ifndef NC_DECODE_BAL_PIECES
-#define NC_DECODE_BAL_PIECES 3136  // balanced grids: at most n_groups + this many workgroups
-#endif
-constexpr int64_t kDecodeBalPieces = NC_DECODE_BAL_PIECES;
 #ifndef NC_DECODE_BAL_MIN_TILES
 #define NC_DECODE_BAL_MIN_TILES 4  // least 64-key tiles per piece
 #endif

@@ -103,10 +103,10 @@ def test_default_decode_grid_is_bounded():
     lib = _ext.lib()
     # 192 (row, kv head) groups (48 rows, GQA 16/4 -> one head block of 4): 4096 // 192 = 21 splits
     # per group instead of 16384 / 256 = 64.  Rows longer than 21 x 256 keys then take
-    # length-balanced pieces, on a grid of min(192 x 21, 192 + 3136) = 3328 workgroups with one
-    # partial slot per workgroup and q head of its block.  An explicit split size keeps every split.
+    # length-balanced pieces, on the same grid of 192 x 21 workgroups with one partial slot per
+    # workgroup and q head of its block.  An explicit split size keeps every split.
     pairs = 48 * 16
-    slots = 3328 * 4
+    slots = 192 * 21 * 4
     a = _attn_args(B=48, T_max=16384, H=16, H_kv=4)
     assert lib.nc_attn_workspace_bytes(ctypes.byref(a)) == \
         _ext.NC_WORKSPACE_SYNC_BYTES + 256 * ((slots * 8 + 255) // 256) + slots * 128 * 4
