@@ -368,7 +368,9 @@ def test_small_m_projections_in_the_model(monkeypatch):
 def test_c1_engine_generate_matches_reference_tokens_fp32_cache(variant):
     """Engine.generate itself (prefill, fan-out, graph-replayed decode, fused prologue, greedy steps on
     the sampling kernel) on the GPU with an fp32 cache reproduces the reference's 64 golden tokens.
-    The perturbed weights make attention and the smear state change the logits."""
+    The perturbed weights make attention and the smear state change the logits: the reference
+    initialises attn.c_proj, mlp.c_proj and smear_lambda to zero (nanochat/gpt.py:228,230,242), so at
+    init the tokens do not depend on the attention outputs."""
     model = c1_model(variant).to(DEV)
     engine = Engine(model, SpecialTokens(), cache_dtype=torch.float32)
     out = [col[0] for col, _ in engine.generate(GOLDEN["prompt"], num_samples=1, max_tokens=64, temperature=0.0)]
